@@ -1,0 +1,236 @@
+/*
+ * turbo_decode_tail.h -- C ABI of the MI355X (gfx950) decode tail.
+ *
+ * Replaces the decode tail of ForwardRunner::produce_token (src/runner.cpp:719-807):
+ *
+ *   final RMSNorm -> affine-int4 tied LM head (group 64, BF16 scale + bias) over the whole
+ *   vocabulary -> final-logit softcap -> logit modifiers -> greedy argmax or sampled draw
+ *
+ * Conventions follow include/gturbo/c_api.h:
+ *   - plain C types and pointers only; every entry point catches all C++ exceptions;
+ *   - handle-returning calls return NULL on failure, int-returning calls return 1 on success
+ *     and 0 on failure; the reason is in turbo_lmhead_last_error() (thread-local, "" after a
+ *     successful call, valid until the next failing call on the same thread; c_api.h:74-78);
+ *   - option structs must be initialised by their *_default() function before use, because
+ *     zero-initialisation is not valid (c_api.h:30-47).
+ *
+ * Memory: unless a comment says "host", every buffer pointer is a HIP device pointer. All
+ * work is enqueued on the handle's stream (turbo_lmhead_set_stream; default: the null stream)
+ * and is asynchronous to the host. One step in flight per handle; calls on one handle must be
+ * serialised by the caller, as the reference serialises generation (README.md:202-206).
+ */
+#ifndef TURBO_DECODE_TAIL_H
+#define TURBO_DECODE_TAIL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TURBO_DT_API __attribute__((visibility("default")))
+
+/* ---- errors ------------------------------------------------------------------------------ */
+
+/* Replaces turbo_engine_last_error (include/gturbo/c_api.h:74-78; src/c_api.cpp:29-40). */
+TURBO_DT_API const char* turbo_lmhead_last_error(void);
+
+/* ---- head creation ----------------------------------------------------------------------- */
+
+/*
+ * Describes the tied LM head and final norm. Field meanings follow the manifest constants
+ * (include/gturbo/manifest.hpp:23-50) and the resident-table layout the reference uploads at
+ * ForwardRunner::initialize (src/runner.cpp:260-292, :324-357):
+ *   weight       [vocab][hidden/2] bytes, element c in byte c/2, low nibble when c is even
+ *                (docs/GTURBO_FORMAT.md:40; shaders/Common.hlsli:27-29)
+ *   scales       [vocab][hidden/64] BF16, row-major
+ *   biases       [vocab][hidden/64] BF16, row-major; dequantised w = q * scale + bias
+ *   norm_weight  [hidden] BF16 model.norm.weight, applied as plain w (not 1 + w,
+ *                src/cpu_reference.cpp:40-42); NULL means no weight
+ */
+typedef struct {
+    uint32_t vocab_size;        /* 262144 for Gemma 4 (manifest.hpp:32) */
+    uint32_t hidden_size;       /* 2816 (manifest.hpp:24); must be a multiple of 64 */
+    uint32_t group_size;        /* must be 64 (src/cpu_reference.cpp:32) */
+    float final_logit_softcap;  /* 30 (manifest.hpp:34); <= 0 disables the softcap */
+    float rms_norm_eps;         /* 1e-6 (manifest.hpp:39) */
+    int weights_on_device;      /* 0: the four pointers are host memory; 1: device memory */
+    const uint8_t* weight;
+    const uint16_t* scales;
+    const uint16_t* biases;
+    const uint16_t* norm_weight;
+    int device;                 /* HIP device ordinal */
+} TurboLMHeadDesc;
+
+/* Fills the Gemma 4 26B-A4B constants; the four pointers are NULL. */
+TURBO_DT_API void turbo_lmhead_desc_default(TurboLMHeadDesc* out);
+
+/*
+ * Copies the table into HBM in the kernels' tiled layout (the caller's buffers may be freed
+ * afterwards) and allocates per-step scratch. Replaces the resident upload and buffer set-up
+ * of ForwardRunner::initialize for this path (src/runner.cpp:211-215, :260-292).
+ * Returns NULL on failure.
+ */
+TURBO_DT_API void* turbo_lmhead_create(const TurboLMHeadDesc* desc);
+/* Drains the stream and frees everything (src/runner.cpp:25-42). NULL is a no-op. */
+TURBO_DT_API void turbo_lmhead_destroy(void* handle);
+/* hip_stream is a hipStream_t (NULL = the null stream). Must be created at default priority. */
+TURBO_DT_API int turbo_lmhead_set_stream(void* handle, void* hip_stream);
+TURBO_DT_API int turbo_lmhead_synchronize(void* handle);
+/* Largest batch one step accepts, and the per-row modifier capacity (history + bias entries). */
+TURBO_DT_API int turbo_lmhead_limits(void* handle, int* max_batch, int* max_row_modifiers);
+
+/* ---- sampling parameters ----------------------------------------------------------------- */
+
+enum {
+    TURBO_RNG_PHILOX = 0,    /* u = Philox4x32-10(key = seed, counter = counter), 24-bit */
+    TURBO_RNG_REFERENCE = 1  /* u = next_uniform(seed_for(has_seed, seed, position = counter)),
+                                the reference's map (src/sampling.cpp:18-28, :63-72) */
+};
+
+enum {
+    /* Lifts the reference's 256-candidate shortlist and accepts top_k == 0 with top_p < 1:
+     * nucleus over the full vocabulary, as the full-sort sampler of
+     * tests/test_sampling.cpp:36-84. Without it the semantics are exactly sample_token's. */
+    TURBO_ROW_FULL_VOCAB = 1u
+};
+
+/*
+ * Per-row sampling parameters. The first four fields are SamplingParams
+ * (include/gturbo/sampling.hpp:21-30); the rest are extensions.
+ */
+typedef struct {
+    float temperature;          /* 0 = greedy */
+    float top_p;                /* (0, 1]; 1 = no nucleus */
+    int top_k;                  /* 0..256; 0 = off */
+    float repetition_penalty;   /* > 0; 1 = off; applied per history occurrence */
+    float presence_penalty;     /* extension: l -= presence for ids seen at least once */
+    float frequency_penalty;    /* extension: l -= frequency * count */
+    int rng;                    /* TURBO_RNG_* */
+    int has_seed;               /* TURBO_RNG_REFERENCE only */
+    uint64_t seed;
+    uint64_t counter;           /* Philox counter (decode step), or the reference position */
+    uint32_t flags;             /* TURBO_ROW_* */
+} TurboSamplingRow;
+
+/* Greedy, no penalties, Philox with seed 0 counter 0 (sampling.hpp:21-30 defaults). */
+TURBO_DT_API void turbo_sampling_row_default(TurboSamplingRow* out);
+/* validate_sampling (src/sampling.cpp:32-54). Returns 1 if valid; else 0 and the reason. */
+TURBO_DT_API int turbo_validate_sampling(const TurboSamplingRow* row);
+/* splitmix64 and seed_for (src/sampling.cpp:56-72). */
+TURBO_DT_API uint64_t turbo_splitmix64(uint64_t x);
+TURBO_DT_API uint64_t turbo_seed_for(int has_seed, uint64_t seed, int position);
+/* The uniform a step draws for this row (host computation of the device's value). */
+TURBO_DT_API float turbo_row_uniform(const TurboSamplingRow* row);
+
+/* ---- the decode-tail step ---------------------------------------------------------------- */
+
+enum { TURBO_HIDDEN_F32 = 0, TURBO_HIDDEN_BF16 = 1 };
+
+enum {
+    TURBO_STEP_NORMED = 1u,          /* hidden is already normalised: skip the final RMSNorm */
+    TURBO_STEP_APPEND_HISTORY = 2u   /* append each row's token to its history on the device
+                                        (src/runner.cpp:878), incrementing history_len */
+};
+
+/* Row-strided side inputs. Any group may be NULL / zero to disable it. */
+typedef struct {
+    int batch;                  /* 1 .. max_batch */
+    const void* hidden;         /* [batch][hidden_size], TURBO_HIDDEN_* (buf_hidden_ at :722) */
+    int hidden_dtype;
+    uint32_t flags;             /* TURBO_STEP_* */
+    const TurboSamplingRow* rows; /* HOST array [batch], copied by the call */
+    /* history ids (src/runner.cpp:801-803): row b has history_len[b] ids at
+     * history + b * history_stride; ids >= vocab are ignored (src/sampling.cpp:82). */
+    uint32_t* history;
+    uint32_t history_stride;
+    uint32_t* history_len;
+    /* banned-token bitmask (extension): bit (id % 32) of word ban_bits[b * ban_stride + id/32] */
+    const uint32_t* ban_bits;
+    uint32_t ban_stride;
+    /* sparse logit bias (extension): bias_count[b] pairs at b * bias_stride */
+    const uint32_t* bias_ids;
+    const float* bias_values;
+    uint32_t bias_stride;
+    const uint32_t* bias_count;
+    /* injected uniforms [batch] in [0, 1); NULL = derive from each row's rng */
+    const float* uniforms;
+} TurboStepInputs;
+
+/* Diagnostics per row (optional). */
+typedef struct {
+    float max_logit;        /* row maximum after modifiers */
+    float u;                /* uniform used */
+    uint32_t shortlist;     /* candidate list size (want) */
+    uint32_t cut;           /* survivors after top-p / top-k */
+    uint32_t rank;          /* token's position among the survivors */
+    uint32_t path;          /* 0 greedy, 1 shortlist, 2 full-vocabulary radix, 3 degenerate */
+    double total;           /* sum exp(l - max) over the row */
+    double denom;           /* survivor weight sum */
+    double r;               /* u * denom */
+} TurboRowReport;
+
+typedef struct {
+    uint32_t* tokens;        /* [batch]; 0xFFFFFFFF marks a degenerate distribution */
+    float* logits;           /* optional [batch][vocab]: final logits after all modifiers */
+    TurboRowReport* report;  /* optional [batch] */
+} TurboStepOutputs;
+
+/*
+ * One decode-tail step for a batch of independent rows: (RMSNorm) -> int4 head -> softcap ->
+ * bias -> repetition -> presence/frequency -> ban -> greedy or sampled token per row.
+ * Replaces src/runner.cpp:719-807 (RMSNormK, LMHeadGreedy + ArgmaxReduce or GemvInt4 x5 +
+ * Softcap + readback + apply_repetition_penalty + sample_token). Every row is validated
+ * first (turbo_validate_sampling); an invalid row fails the call before anything is enqueued.
+ */
+TURBO_DT_API int turbo_lmhead_step(void* handle, const TurboStepInputs* in,
+                                   const TurboStepOutputs* out);
+
+/* ---- kernel-level entry points (one per reference kernel on the path) -------------------- */
+
+/* RMSNormK with model.norm.weight (shaders/RMSNormK.hlsl:25-61; src/cpu_reference.cpp:43-52).
+ * x, out: [batch][hidden] FP32. */
+TURBO_DT_API int turbo_lmhead_rms_norm(void* handle, const float* x, int batch, float* out);
+
+/* GemvInt4 over the tied table (shaders/GemvInt4.hlsl:18-38, src/runner.cpp:429-442, :773),
+ * followed by Softcap when apply_softcap (shaders/Softcap.hlsl:18-30, src/runner.cpp:774-779).
+ * x: [batch][hidden] (TURBO_HIDDEN_*, already normalised), logits: [batch][vocab] FP32. */
+TURBO_DT_API int turbo_lmhead_logits(void* handle, const void* x, int x_dtype, int batch,
+                                     int apply_softcap, float* logits);
+
+/* LMHeadGreedy + ArgmaxReduce (shaders/LMHeadGreedy.hlsl:28-73, ArgmaxReduce.hlsl:21-62):
+ * argmax of the softcapped logits, ties to the lowest row. tokens: [batch]. */
+TURBO_DT_API int turbo_lmhead_greedy(void* handle, const void* x, int x_dtype, int batch,
+                                     uint32_t* tokens);
+
+/* Softcap in place on n floats (shaders/Softcap.hlsl:18-30). stream may be NULL. */
+TURBO_DT_API int turbo_softcap(void* hip_stream, float* z, size_t n, float cap);
+
+/* apply_repetition_penalty in place on one row (src/sampling.cpp:74-90). stream may be NULL. */
+TURBO_DT_API int turbo_apply_repetition_penalty(void* hip_stream, float* logits, uint32_t vocab,
+                                                const uint32_t* history, uint32_t n,
+                                                float penalty, float softcap);
+
+/*
+ * Sampling on caller-provided logits (sample_token, src/sampling.cpp:92-169, plus the
+ * modifiers of turbo_lmhead_step). logits: [batch][vocab], modified in place by the
+ * modifiers. in->hidden and in->hidden_dtype are ignored. out->logits is ignored.
+ */
+TURBO_DT_API int turbo_sample_logits(void* handle, float* logits, const TurboStepInputs* in,
+                                     const TurboStepOutputs* out);
+
+/* ---- measurement ------------------------------------------------------------------------- */
+
+/* When enabled, HIP events bracket every launch of the head kernel (the int4 GEMV / MFMA
+ * kernel) on the handle's stream. turbo_lmhead_head_kernel_time synchronises and returns the
+ * summed milliseconds and launch count since the last reset. */
+TURBO_DT_API int turbo_lmhead_enable_head_timing(void* handle, int enable);
+TURBO_DT_API int turbo_lmhead_head_kernel_time(void* handle, double* total_ms, int* launches,
+                                               int reset);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TURBO_DECODE_TAIL_H */

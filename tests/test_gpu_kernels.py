@@ -1,0 +1,155 @@
+"""GPU parity of each kernel-level entry point against the oracle, at sizes the oracle finishes in
+seconds. Mirrors the reference's tests/test_gpu_kernels.cpp sections for this path."""
+import numpy as np
+import pytest
+
+import orc_py as O
+import parity_util as U
+import synth
+import turbo_decode_tail as T
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+V_SMALL, D = 16384, 2816
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+@pytest.fixture(scope="module")
+def small_head():
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    W, S, B, g = synth.make_head(V_SMALL, D, 101)
+    h = T.LMHead(W, S, B, g, vocab=V_SMALL, hidden=D)
+    yield h, (W, S, B, g)
+    h.close()
+
+
+def test_rms_norm_matches_oracle(small_head):
+    h, (W, S, B, g) = small_head
+    x = synth.hidden_states(3, D, 5)
+    out = torch.empty((3, D), dtype=torch.float32, device="cuda")
+    h.rms_norm(dev(x), 3, out)
+    h.sync()
+    got = out.cpu().numpy()
+    for b in range(3):
+        want = O.rms_norm(x[b], g, 1e-6)
+        # same operation sequence (double sum, float 1/sqrt, x*inv*w); the double sum's order
+        # differs, so allow one ulp
+        assert np.max(np.abs(got[b] - want) / np.maximum(np.abs(want), 1e-30)) <= 2.0**-23
+
+
+@pytest.mark.parametrize("batch", [1, 2])
+def test_logits_digit_path(small_head, batch):
+    """GemvInt4 + Softcap at B <= 2: the reference's own tolerance (allclose 1e-5 + 1e-4 |want|)."""
+    h, (W, S, B, g) = small_head
+    x = np.stack([O.rms_norm(r, g, 1e-6) for r in synth.hidden_states(batch, D, 6)])
+    out = torch.empty((batch, V_SMALL), dtype=torch.float32, device="cuda")
+    h.logits(dev(x), batch, out)
+    h.sync()
+    got = out.cpu().numpy()
+    for b in range(batch):
+        want = O.softcap(O.matvec(W, S, B, x[b], U.THREADS), 30.0)
+        err = np.abs(got[b] - want)
+        assert np.all(err <= 1e-5 + 1e-4 * np.abs(want)), float(np.max(err))
+        raw = torch.empty((1, V_SMALL), dtype=torch.float32, device="cuda")
+        h.logits(dev(x[b:b + 1]), 1, raw, softcap=False)
+        h.sync()
+        want_raw = O.matvec(W, S, B, x[b], U.THREADS)
+        assert np.all(np.abs(raw.cpu().numpy()[0] - want_raw) <= 1e-5 + 1e-4 * np.abs(want_raw))
+
+
+@pytest.mark.parametrize("batch", [3, 32, 64, 100, 256])
+def test_logits_mfma_path(small_head, batch):
+    """Batched head: fp16-dequantised weights, fp32 accumulation, 2e-3 relative (RMS floor)."""
+    h, (W, S, B, g) = small_head
+    x = np.stack([O.rms_norm(r, g, 1e-6) for r in synth.hidden_states(batch, D, 7)])
+    out = torch.empty((batch, V_SMALL), dtype=torch.float32, device="cuda")
+    h.logits(dev(x), batch, out)
+    h.sync()
+    got = out.cpu().numpy()
+    rows = sorted({0, 1, batch // 2, batch - 1})
+    for b in rows:
+        want = O.softcap(O.matvec(W, S, B, x[b], U.THREADS), 30.0)
+        e = U.logit_err(got[b], want)
+        assert e <= U.LOGIT_RTOL, (b, e)
+
+
+def test_logits_mfma_bf16_input(small_head):
+    h, (W, S, B, g) = small_head
+    xb = synth.f32_to_bf16(synth.hidden_states(8, D, 8))
+    out = torch.empty((8, V_SMALL), dtype=torch.float32, device="cuda")
+    h.logits(dev(xb.view(np.int16)), 8, out, dtype=T.TURBO_HIDDEN_BF16)
+    h.sync()
+    got = out.cpu().numpy()
+    for b in (0, 7):
+        want = O.softcap(O.matvec(W, S, B, synth.bf16_to_f32(xb[b]), U.THREADS), 30.0)
+        assert U.logit_err(got[b], want) <= U.LOGIT_RTOL
+
+
+def test_greedy_matches_full_gemv_argmax():
+    """LMHeadGreedy + ArgmaxReduce (tests/test_gpu_kernels.cpp:743-802): 4096 x 2816, x ~ U(-1.5,1.5)."""
+    W, S, B, g = synth.make_head(4096, D, 12345)
+    h = T.LMHead(W, S, B, None, vocab=4096, hidden=D)
+    try:
+        for seed in range(4):
+            x = (synth.uniform(seed, 70, D) * 3.0 - 1.5).astype(np.float32)
+            tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+            h.greedy(dev(x[None]), 1, tok)
+            h.sync()
+            want = O.softcap(O.matvec(W, S, B, x), 30.0)
+            if U.greedy_near_tie(want):
+                continue
+            assert int(tok.item()) == int(np.argmax(want))
+    finally:
+        h.close()
+
+
+def test_greedy_ties_go_to_lowest_row():
+    """Rows 5, 77 and 1000 are identical and hold the maximum: the lowest index must win."""
+    V = 2048
+    W, S, B, _ = synth.make_head(V, D, 3)
+    x = synth.hidden_states(1, D, 9)[0]
+    q = np.where(x > 0, 15, 0).astype(np.uint8)
+    row = (q[0::2] | (q[1::2] << 4)).astype(np.uint8)
+    for r in (1000, 77, 5):
+        W[r] = row
+        S[r] = synth.f32_to_bf16(np.full(D // 64, 0.01, np.float32))
+        B[r] = 0
+    want = O.softcap(O.matvec(W, S, B, x), 30.0)
+    assert want[5] == want[77] == want[1000] == want.max()
+    h = T.LMHead(W, S, B, None, vocab=V, hidden=D)
+    try:
+        tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+        h.greedy(dev(x[None]), 1, tok)
+        h.sync()
+        assert int(tok.item()) == 5
+    finally:
+        h.close()
+
+
+def test_softcap_kernel():
+    z = (synth.uniform(1, 71, 4096) * 400 - 200).astype(np.float32)  # U(-200, 200) as :389-411
+    t = torch.from_numpy(z).cuda()
+    T.softcap(t, z.size, 30.0)
+    torch.cuda.synchronize()
+    want = O.softcap(z, 30.0)
+    got = t.cpu().numpy()
+    assert np.all(np.abs(got - want) <= 1e-5 + 1e-4 * np.abs(want))
+    assert np.all(got[np.abs(z) > 300] == np.sign(z[np.abs(z) > 300]) * 30.0)
+
+
+def test_repetition_penalty_kernel():
+    V = 262144
+    for (n, p) in [(256, 1.1), (2048, 1.15), (5000, 0.8), (0, 2.0)]:
+        l = (synth.normal(n, 72, V) * 10).astype(np.float32)
+        hist = synth.zipf_ids(max(n, 1), V + 100, 1.1, n)[:n]  # duplicates and out-of-range ids
+        t = torch.from_numpy(l).cuda()
+        T.apply_repetition_penalty(t, V, torch.from_numpy(hist.astype(np.int32)).cuda() if n else None,
+                                   n, p, 30.0)
+        torch.cuda.synchronize()
+        want = l.copy()
+        O.orc().orc_apply_repetition_penalty(want, V, hist.ctypes.data if n else None, n, p, 30.0)
+        assert np.array_equal(t.cpu().numpy(), want)

@@ -1,0 +1,665 @@
+// C ABI of the decode tail (include/turbo_decode_tail.h).
+//
+// Mirrors the conventions of the reference C API (src/c_api.cpp): a thread-local last error,
+// NULL / 0 on failure, every entry point catching all exceptions. The host-side numerics that
+// the reference keeps on the CPU (validate_sampling, splitmix64, seed_for, the per-token
+// uniform; src/sampling.cpp:18-72) are restated here; everything else is enqueued on the GPU.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <stdexcept>
+#include <string>
+
+#include "../../include/turbo_decode_tail.h"
+#include "dt_internal.h"
+
+namespace tdt {
+
+void check_hip(hipError_t e, const char* what) {
+    if (e != hipSuccess) {
+        throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+    }
+}
+
+}  // namespace tdt
+
+using tdt::Head;
+using tdt::check_hip;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+void set_error(const std::string& m) { g_last_error = m; }
+void clear_error() { g_last_error.clear(); }
+
+constexpr int kMaxBatch = 256;
+constexpr uint32_t kModCap = 8192;  // history + bias entries per row (64 KiB of LDS sort keys)
+
+struct HandleBox {
+    uint32_t magic = 0x54445448u;  // "TDTH"
+    Head h;
+    double t_accum_ms = 0.0;
+    int t_accum_n = 0;
+};
+
+HandleBox* box(void* p) {
+    if (!p) throw std::runtime_error("null handle");
+    auto* b = static_cast<HandleBox*>(p);
+    if (b->magic != 0x54445448u) throw std::runtime_error("invalid handle");
+    return b;
+}
+
+template <typename T>
+T* dalloc(size_t count, const char* what) {
+    void* p = nullptr;
+    check_hip(hipMalloc(&p, std::max<size_t>(count, 1) * sizeof(T)), what);
+    return static_cast<T*>(p);
+}
+
+void dfree(void* p) {
+    if (p) (void)hipFree(p);
+}
+
+// ---- host restatement of the reference's scalar sampling helpers ---------------------------
+
+uint64_t splitmix64_h(uint64_t x) {  // src/sampling.cpp:56-61
+    x += 0x9E3779B97F4A7C15ULL;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBULL;
+    return x ^ (x >> 31);
+}
+
+uint64_t seed_for_h(int has_seed, uint64_t seed, int position) {  // src/sampling.cpp:63-72
+    const uint64_t base = has_seed ? seed + static_cast<uint64_t>(static_cast<int64_t>(position))
+                                   : (0x9E3779B97F4A7C15ULL ^
+                                      (static_cast<uint64_t>(static_cast<int64_t>(position)) *
+                                       0xD1B54A32D192ED03ULL));
+    const uint64_t s = splitmix64_h(base);
+    return s ? s : 0x9E3779B97F4A7C15ULL;
+}
+
+float xorshift_uniform(uint64_t state) {  // src/sampling.cpp:18-28
+    state ^= state >> 12;
+    state ^= state << 25;
+    state ^= state >> 27;
+    const uint64_t r = state * 0x2545F4914F6CDD1DULL;
+    return static_cast<float>((r >> 40) & 0xFFFFFF) / 16777216.0f;
+}
+
+float row_uniform(const TurboSamplingRow& r) {
+    if (r.rng == TURBO_RNG_REFERENCE)
+        return xorshift_uniform(seed_for_h(r.has_seed, r.seed, static_cast<int>(r.counter)));
+    const uint32_t x = tdt::philox4x32_10_x(r.counter, r.seed);
+    return static_cast<float>(x >> 8) / 16777216.0f;
+}
+
+// validate_sampling (src/sampling.cpp:32-54) plus the extension fields.
+bool validate_row(const TurboSamplingRow& p, std::string* why) {
+    if (!std::isfinite(p.temperature) || p.temperature < 0.0f) {
+        *why = "temperature must be finite and >= 0 (0 = greedy)";
+        return false;
+    }
+    if (!std::isfinite(p.top_p) || p.top_p <= 0.0f || p.top_p > 1.0f) {
+        *why = "top_p must be in (0, 1]";
+        return false;
+    }
+    if (p.top_k < 0 || p.top_k > static_cast<int>(tdt::kMaxTopK)) {
+        *why = "top_k must be in 0..256 (0 disables it)";
+        return false;
+    }
+    if (!std::isfinite(p.repetition_penalty) || p.repetition_penalty <= 0.0f) {
+        *why = "repetition_penalty must be finite and > 0 (1 = disabled)";
+        return false;
+    }
+    if (!std::isfinite(p.presence_penalty) || !std::isfinite(p.frequency_penalty)) {
+        *why = "presence_penalty and frequency_penalty must be finite";
+        return false;
+    }
+    if (p.rng != TURBO_RNG_PHILOX && p.rng != TURBO_RNG_REFERENCE) {
+        *why = "rng must be TURBO_RNG_PHILOX or TURBO_RNG_REFERENCE";
+        return false;
+    }
+    if ((p.flags & ~static_cast<uint32_t>(TURBO_ROW_FULL_VOCAB)) != 0u) {
+        *why = "unknown row flags";
+        return false;
+    }
+    if (!(p.flags & TURBO_ROW_FULL_VOCAB) && p.temperature > 0.0f && p.top_p < 1.0f &&
+        p.top_k == 0) {
+        *why = "top_p < 1 with temperature > 0 requires top_k in 1..256; full-vocabulary nucleus "
+               "sampling needs TURBO_ROW_FULL_VOCAB";
+        return false;
+    }
+    return true;
+}
+
+void free_head(Head& h) {
+    if (h.stream || h.Wt) (void)hipDeviceSynchronize();
+    dfree(h.Wt);
+    dfree(h.SBt);
+    dfree(h.gamma);
+    dfree(h.xn);
+    dfree(h.xdig);
+    dfree(h.xws);
+    dfree(h.xsum);
+    dfree(h.x16);
+    dfree(h.logits);
+    dfree(h.partials);
+    dfree(h.rows);
+    dfree(h.mods);
+    dfree(h.mod_count);
+    dfree(h.block_start);
+    dfree(h.list_scratch);
+    if (h.ring_host) (void)hipHostFree(h.ring_host);
+    for (int i = 0; i < Head::kRing; ++i)
+        if (h.ring_ev[i]) (void)hipEventDestroy(h.ring_ev[i]);
+    for (int i = 0; i < Head::kTimerSlots; ++i) {
+        if (h.t_start[i]) (void)hipEventDestroy(h.t_start[i]);
+        if (h.t_stop[i]) (void)hipEventDestroy(h.t_stop[i]);
+    }
+}
+
+// Copies B DevRows through the pinned ring onto the device row buffer (stream-ordered).
+void upload_rows(Head& h, const tdt::DevRow* rows, int B) {
+    const int pos = h.ring_pos;
+    h.ring_pos = (h.ring_pos + 1) % Head::kRing;
+    check_hip(hipEventSynchronize(h.ring_ev[pos]), "row staging wait");
+    tdt::DevRow* slot = h.ring_host + static_cast<size_t>(pos) * h.max_batch;
+    std::memcpy(slot, rows, sizeof(tdt::DevRow) * B);
+    check_hip(hipMemcpyAsync(h.rows, slot, sizeof(tdt::DevRow) * B, hipMemcpyHostToDevice,
+                             h.stream),
+              "row upload");
+    check_hip(hipEventRecord(h.ring_ev[pos], h.stream), "row staging record");
+}
+
+tdt::DevRow make_devrow(const Head& h, const TurboSamplingRow& r, uint32_t has_mods) {
+    tdt::DevRow d{};
+    d.temperature = r.temperature;
+    d.top_p = r.top_p;
+    d.top_k = r.top_k;
+    d.repetition_penalty = r.repetition_penalty;
+    d.presence_penalty = r.presence_penalty;
+    d.frequency_penalty = r.frequency_penalty;
+    d.u = row_uniform(r);
+    d.flags = r.flags;
+    if (r.top_k > 0) d.want = std::min<uint32_t>(static_cast<uint32_t>(r.top_k), h.V);
+    else if (r.flags & TURBO_ROW_FULL_VOCAB) d.want = h.V;
+    else d.want = std::min<uint32_t>(tdt::kMaxTopK, h.V);
+    d.has_mods = has_mods;
+    return d;
+}
+
+tdt::DevRow greedy_devrow(const Head& h) {
+    TurboSamplingRow r;
+    turbo_sampling_row_default(&r);
+    return make_devrow(h, r, 0u);
+}
+
+tdt::EpiArgs epi_args(const Head& h, float* logits, bool softcap) {
+    tdt::EpiArgs ep{};
+    ep.V = h.V;
+    ep.ntile = h.ntile;
+    ep.cap = softcap ? h.cap : 0.0f;
+    ep.logits = logits;
+    ep.partials = h.partials;
+    ep.rows = h.rows;
+    ep.mods = h.mods;
+    ep.mod_cap = h.mod_cap;
+    ep.block_start = h.block_start;
+    ep.ban = nullptr;
+    ep.ban_stride = 0;
+    ep.rep_limit = (h.cap > 0.0f) ? h.cap * 0.9999f : 0.0f;
+    return ep;
+}
+
+void launch_head(HandleBox& bx, int B, const tdt::EpiArgs& ep) {
+    Head& h = bx.h;
+    const bool timed = h.timing;
+    if (timed && h.t_count >= Head::kTimerSlots) {
+        check_hip(hipStreamSynchronize(h.stream), "timer fold");
+        for (int i = 0; i < h.t_count; ++i) {
+            float ms = 0.f;
+            check_hip(hipEventElapsedTime(&ms, h.t_start[i], h.t_stop[i]), "timer read");
+            bx.t_accum_ms += ms;
+        }
+        bx.t_accum_n += h.t_count;
+        h.t_count = 0;
+    }
+    if (timed) check_hip(hipEventRecord(h.t_start[h.t_count], h.stream), "timer start");
+    if (B <= 2) tdt::launch_head_digits(h, B, ep, h.stream);
+    else tdt::launch_head_mfma(h, B, ep, h.stream);
+    if (timed) {
+        check_hip(hipEventRecord(h.t_stop[h.t_count], h.stream), "timer stop");
+        ++h.t_count;
+    }
+}
+
+tdt::HeadPath path_for(int B) { return B <= 2 ? tdt::HeadPath::Digits : tdt::HeadPath::Mfma; }
+
+void check_batch(const Head& h, int B) {
+    if (B < 1 || B > h.max_batch)
+        throw std::runtime_error("batch must be in 1.." + std::to_string(h.max_batch));
+}
+
+// Shared by turbo_lmhead_step and turbo_sample_logits.
+int run_rows(HandleBox& bx, const TurboStepInputs* in, const TurboStepOutputs* out,
+             const void* hidden, float* given_logits) {
+    Head& h = bx.h;
+    if (!in || !out) throw std::runtime_error("null inputs or outputs");
+    const int B = in->batch;
+    check_batch(h, B);
+    if (!in->rows) throw std::runtime_error("rows is NULL");
+    if (!out->tokens) throw std::runtime_error("out->tokens is NULL");
+    if (hidden && in->hidden_dtype != TURBO_HIDDEN_F32 && in->hidden_dtype != TURBO_HIDDEN_BF16)
+        throw std::runtime_error("hidden_dtype must be TURBO_HIDDEN_F32 or TURBO_HIDDEN_BF16");
+    const bool has_hist = in->history && in->history_len && in->history_stride > 0;
+    const bool has_bias = in->bias_ids && in->bias_values && in->bias_count && in->bias_stride > 0;
+    if ((in->flags & TURBO_STEP_APPEND_HISTORY) && !has_hist)
+        throw std::runtime_error("TURBO_STEP_APPEND_HISTORY needs history, history_len and history_stride");
+    if (in->ban_bits && in->ban_stride < (h.V + 31u) / 32u)
+        throw std::runtime_error("ban_stride must be at least ceil(vocab / 32) words");
+
+    tdt::DevRow rows[kMaxBatch];
+    bool all_greedy = true, any_mods = false;
+    for (int b = 0; b < B; ++b) {
+        const TurboSamplingRow& r = in->rows[b];
+        std::string why;
+        if (!validate_row(r, &why)) throw std::runtime_error("row " + std::to_string(b) + ": " + why);
+        const bool uses_hist = has_hist && (r.repetition_penalty != 1.0f ||
+                                            r.presence_penalty != 0.0f || r.frequency_penalty != 0.0f);
+        const uint32_t mods = (uses_hist ? 1u : 0u) | (has_bias ? 2u : 0u);
+        any_mods = any_mods || mods != 0u;
+        all_greedy = all_greedy && r.temperature <= 0.0f;
+        rows[b] = make_devrow(h, r, mods);
+    }
+    if (any_mods) {
+        const uint32_t n = (has_hist ? in->history_stride : 0u) + (has_bias ? in->bias_stride : 0u);
+        if (n > h.mod_cap)
+            throw std::runtime_error("history_stride + bias_stride exceeds " + std::to_string(h.mod_cap));
+    }
+    upload_rows(h, rows, B);
+
+    float* logits = given_logits ? given_logits : (out->logits ? out->logits : (all_greedy ? nullptr : h.logits));
+    if (hidden) {
+        tdt::launch_prep(h, hidden, in->hidden_dtype, B, (in->flags & TURBO_STEP_NORMED) != 0,
+                         nullptr, path_for(B), h.stream);
+    }
+    if (any_mods)
+        tdt::launch_modtable(h, B, has_hist ? in->history : nullptr, in->history_stride,
+                             in->history_len, has_bias ? in->bias_ids : nullptr, in->bias_values,
+                             in->bias_stride, in->bias_count, h.stream);
+    tdt::EpiArgs ep = epi_args(h, logits, hidden != nullptr);
+    ep.ban = in->ban_bits;
+    ep.ban_stride = in->ban_stride;
+    if (hidden) launch_head(bx, B, ep);
+    else tdt::launch_logits_epilogue(h, B, ep, h.stream);
+
+    tdt::SelectArgs sa{};
+    sa.V = h.V;
+    sa.ntile = h.ntile;
+    sa.logits = logits;
+    sa.partials = h.partials;
+    sa.rows = h.rows;
+    sa.uniforms = in->uniforms;
+    sa.tokens = out->tokens;
+    sa.report = out->report;
+    if (in->flags & TURBO_STEP_APPEND_HISTORY) {
+        sa.history = in->history;
+        sa.hist_stride = in->history_stride;
+        sa.hist_len = in->history_len;
+    }
+    tdt::launch_select(h, B, sa, h.stream);
+    return 1;
+}
+
+}  // namespace
+
+#define API_TRY try {
+#define API_CATCH(ret)                                   \
+    }                                                    \
+    catch (const std::exception& ex) {                   \
+        set_error(ex.what());                            \
+        return ret;                                      \
+    }                                                    \
+    catch (...) {                                        \
+        set_error("unknown error");                      \
+        return ret;                                      \
+    }
+
+extern "C" {
+
+TURBO_DT_API const char* turbo_lmhead_last_error(void) { return g_last_error.c_str(); }
+
+TURBO_DT_API void turbo_lmhead_desc_default(TurboLMHeadDesc* out) {
+    if (!out) return;
+    std::memset(out, 0, sizeof(*out));
+    out->vocab_size = 262144;
+    out->hidden_size = 2816;
+    out->group_size = 64;
+    out->final_logit_softcap = 30.0f;
+    out->rms_norm_eps = 1e-6f;
+    out->weights_on_device = 0;
+    out->device = 0;
+}
+
+TURBO_DT_API void* turbo_lmhead_create(const TurboLMHeadDesc* d) {
+    clear_error();
+    API_TRY
+    if (!d) throw std::runtime_error("null descriptor");
+    if (d->group_size != 64) throw std::runtime_error("group_size must be 64");
+    if (d->hidden_size == 0 || d->hidden_size % 64 != 0 || d->hidden_size > 8192)
+        throw std::runtime_error("hidden_size must be a positive multiple of 64, at most 8192");
+    if (d->vocab_size == 0 || d->vocab_size > (1u << 24))
+        throw std::runtime_error("vocab_size must be in 1..16777216");
+    if (!d->weight || !d->scales || !d->biases) throw std::runtime_error("weight/scales/biases are NULL");
+    if (!std::isfinite(d->final_logit_softcap) || !std::isfinite(d->rms_norm_eps) || d->rms_norm_eps < 0.f)
+        throw std::runtime_error("softcap and eps must be finite, eps >= 0");
+
+    auto bx = std::make_unique<HandleBox>();
+    Head& h = bx->h;
+    try {
+        int ndev = 0;
+        check_hip(hipGetDeviceCount(&ndev), "hipGetDeviceCount");
+        if (d->device < 0 || d->device >= ndev) throw std::runtime_error("no such HIP device");
+        check_hip(hipSetDevice(d->device), "hipSetDevice");
+        h.device = d->device;
+        h.V = d->vocab_size;
+        h.D = d->hidden_size;
+        h.G = h.D / 64u;
+        h.NC = h.D / 32u;
+        h.ntile = (h.V + tdt::kTileRows - 1u) / tdt::kTileRows;
+        h.cap = d->final_logit_softcap > 0.f ? d->final_logit_softcap : 0.f;
+        h.eps = d->rms_norm_eps;
+        h.stream = nullptr;
+        h.max_batch = kMaxBatch;
+        h.mod_cap = kModCap;
+
+        const size_t wbytes = static_cast<size_t>(h.V) * (h.D / 2u);
+        const size_t gcount = static_cast<size_t>(h.V) * h.G;
+        h.Wt = dalloc<uint4>(static_cast<size_t>(h.ntile) * h.NC * tdt::kTileRows, "alloc Wt");
+        h.SBt = dalloc<uint32_t>(static_cast<size_t>(h.ntile) * h.G * tdt::kTileRows, "alloc SBt");
+
+        const uint8_t* W = d->weight;
+        const uint16_t* S = d->scales;
+        const uint16_t* Bi = d->biases;
+        uint8_t* tW = nullptr;
+        uint16_t* tS = nullptr;
+        uint16_t* tB = nullptr;
+        if (!d->weights_on_device) {
+            tW = dalloc<uint8_t>(wbytes, "alloc staging W");
+            tS = dalloc<uint16_t>(gcount, "alloc staging S");
+            tB = dalloc<uint16_t>(gcount, "alloc staging B");
+            check_hip(hipMemcpy(tW, d->weight, wbytes, hipMemcpyHostToDevice), "upload W");
+            check_hip(hipMemcpy(tS, d->scales, gcount * 2, hipMemcpyHostToDevice), "upload S");
+            check_hip(hipMemcpy(tB, d->biases, gcount * 2, hipMemcpyHostToDevice), "upload B");
+            W = tW;
+            S = tS;
+            Bi = tB;
+        }
+        tdt::launch_repack(h, W, S, Bi, nullptr);
+        check_hip(hipDeviceSynchronize(), "repack");
+        dfree(tW);
+        dfree(tS);
+        dfree(tB);
+
+        if (d->norm_weight) {
+            h.gamma = dalloc<uint16_t>(h.D, "alloc gamma");
+            check_hip(hipMemcpy(h.gamma, d->norm_weight, h.D * 2u,
+                                d->weights_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice),
+                      "upload gamma");
+        }
+        const size_t MB = static_cast<size_t>(h.max_batch);
+        h.xn = dalloc<float>(MB * h.D, "alloc xn");
+        h.xdig = dalloc<uint32_t>(MB * h.NC * tdt::kDigitWordsPerChunk, "alloc xdig");
+        h.xws = dalloc<float>(MB * h.G, "alloc xws");
+        h.xsum = dalloc<float>(MB * h.G, "alloc xsum");
+        h.x16 = dalloc<uint16_t>(MB * h.D, "alloc x16");
+        h.logits = dalloc<float>(MB * h.V, "alloc logits");
+        h.partials = dalloc<tdt::BlockPartial>(MB * h.ntile, "alloc partials");
+        h.rows = dalloc<tdt::DevRow>(MB, "alloc rows");
+        h.mods = dalloc<tdt::ModEntry>(MB * h.mod_cap, "alloc mods");
+        h.mod_count = dalloc<uint32_t>(MB, "alloc mod_count");
+        h.block_start = dalloc<uint32_t>(MB * (h.ntile + 1u), "alloc block_start");
+        h.list_scratch = dalloc<uint2>(MB * h.V, "alloc list scratch");
+        check_hip(hipHostMalloc(reinterpret_cast<void**>(&h.ring_host),
+                                sizeof(tdt::DevRow) * MB * Head::kRing, hipHostMallocDefault),
+                  "alloc pinned ring");
+        for (int i = 0; i < Head::kRing; ++i)
+            check_hip(hipEventCreateWithFlags(&h.ring_ev[i], hipEventDisableTiming), "ring events");
+        check_hip(hipDeviceSynchronize(), "create");
+    } catch (...) {
+        free_head(h);
+        throw;
+    }
+    return bx.release();
+    API_CATCH(nullptr)
+}
+
+TURBO_DT_API void turbo_lmhead_destroy(void* handle) {
+    if (!handle) return;
+    try {
+        HandleBox* b = box(handle);
+        (void)hipSetDevice(b->h.device);
+        free_head(b->h);
+        b->magic = 0;
+        delete b;
+    } catch (...) {
+    }
+}
+
+TURBO_DT_API int turbo_lmhead_set_stream(void* handle, void* stream) {
+    clear_error();
+    API_TRY
+    box(handle)->h.stream = static_cast<hipStream_t>(stream);
+    return 1;
+    API_CATCH(0)
+}
+
+TURBO_DT_API int turbo_lmhead_synchronize(void* handle) {
+    clear_error();
+    API_TRY
+    Head& h = box(handle)->h;
+    check_hip(hipSetDevice(h.device), "hipSetDevice");
+    check_hip(hipStreamSynchronize(h.stream), "synchronize");
+    return 1;
+    API_CATCH(0)
+}
+
+TURBO_DT_API int turbo_lmhead_limits(void* handle, int* max_batch, int* max_row_modifiers) {
+    clear_error();
+    API_TRY
+    Head& h = box(handle)->h;
+    if (max_batch) *max_batch = h.max_batch;
+    if (max_row_modifiers) *max_row_modifiers = static_cast<int>(h.mod_cap);
+    return 1;
+    API_CATCH(0)
+}
+
+TURBO_DT_API void turbo_sampling_row_default(TurboSamplingRow* out) {
+    if (!out) return;
+    std::memset(out, 0, sizeof(*out));
+    out->temperature = 0.0f;
+    out->top_p = 1.0f;
+    out->top_k = 0;
+    out->repetition_penalty = 1.0f;
+    out->presence_penalty = 0.0f;
+    out->frequency_penalty = 0.0f;
+    out->rng = TURBO_RNG_PHILOX;
+    out->has_seed = 0;
+    out->seed = 0;
+    out->counter = 0;
+    out->flags = 0;
+}
+
+TURBO_DT_API int turbo_validate_sampling(const TurboSamplingRow* row) {
+    clear_error();
+    API_TRY
+    if (!row) throw std::runtime_error("null row");
+    std::string why;
+    if (!validate_row(*row, &why)) throw std::runtime_error(why);
+    return 1;
+    API_CATCH(0)
+}
+
+TURBO_DT_API uint64_t turbo_splitmix64(uint64_t x) { return splitmix64_h(x); }
+
+TURBO_DT_API uint64_t turbo_seed_for(int has_seed, uint64_t seed, int position) {
+    return seed_for_h(has_seed, seed, position);
+}
+
+TURBO_DT_API float turbo_row_uniform(const TurboSamplingRow* row) {
+    if (!row) return 0.0f;
+    return row_uniform(*row);
+}
+
+TURBO_DT_API int turbo_lmhead_step(void* handle, const TurboStepInputs* in,
+                                   const TurboStepOutputs* out) {
+    clear_error();
+    API_TRY
+    HandleBox* bx = box(handle);
+    check_hip(hipSetDevice(bx->h.device), "hipSetDevice");
+    if (!in || !in->hidden) throw std::runtime_error("hidden is NULL");
+    return run_rows(*bx, in, out, in->hidden, nullptr);
+    API_CATCH(0)
+}
+
+TURBO_DT_API int turbo_sample_logits(void* handle, float* logits, const TurboStepInputs* in,
+                                     const TurboStepOutputs* out) {
+    clear_error();
+    API_TRY
+    HandleBox* bx = box(handle);
+    check_hip(hipSetDevice(bx->h.device), "hipSetDevice");
+    if (!logits) throw std::runtime_error("logits is NULL");
+    return run_rows(*bx, in, out, nullptr, logits);
+    API_CATCH(0)
+}
+
+TURBO_DT_API int turbo_lmhead_rms_norm(void* handle, const float* x, int batch, float* out) {
+    clear_error();
+    API_TRY
+    Head& h = box(handle)->h;
+    check_hip(hipSetDevice(h.device), "hipSetDevice");
+    check_batch(h, batch);
+    if (!x || !out) throw std::runtime_error("x or out is NULL");
+    tdt::launch_prep(h, x, TURBO_HIDDEN_F32, batch, false, out, tdt::HeadPath::Digits, h.stream);
+    return 1;
+    API_CATCH(0)
+}
+
+TURBO_DT_API int turbo_lmhead_logits(void* handle, const void* x, int x_dtype, int batch,
+                                     int apply_softcap, float* logits) {
+    clear_error();
+    API_TRY
+    HandleBox* bx = box(handle);
+    Head& h = bx->h;
+    check_hip(hipSetDevice(h.device), "hipSetDevice");
+    check_batch(h, batch);
+    if (!x || !logits) throw std::runtime_error("x or logits is NULL");
+    if (x_dtype != TURBO_HIDDEN_F32 && x_dtype != TURBO_HIDDEN_BF16)
+        throw std::runtime_error("x_dtype must be TURBO_HIDDEN_F32 or TURBO_HIDDEN_BF16");
+    tdt::DevRow rows[kMaxBatch];
+    for (int b = 0; b < batch; ++b) rows[b] = greedy_devrow(h);
+    upload_rows(h, rows, batch);
+    tdt::launch_prep(h, x, x_dtype, batch, true, nullptr, path_for(batch), h.stream);
+    launch_head(*bx, batch, epi_args(h, logits, apply_softcap != 0));
+    return 1;
+    API_CATCH(0)
+}
+
+TURBO_DT_API int turbo_lmhead_greedy(void* handle, const void* x, int x_dtype, int batch,
+                                     uint32_t* tokens) {
+    clear_error();
+    API_TRY
+    HandleBox* bx = box(handle);
+    Head& h = bx->h;
+    check_hip(hipSetDevice(h.device), "hipSetDevice");
+    check_batch(h, batch);
+    if (!x || !tokens) throw std::runtime_error("x or tokens is NULL");
+    if (x_dtype != TURBO_HIDDEN_F32 && x_dtype != TURBO_HIDDEN_BF16)
+        throw std::runtime_error("x_dtype must be TURBO_HIDDEN_F32 or TURBO_HIDDEN_BF16");
+    tdt::DevRow rows[kMaxBatch];
+    for (int b = 0; b < batch; ++b) rows[b] = greedy_devrow(h);
+    upload_rows(h, rows, batch);
+    tdt::launch_prep(h, x, x_dtype, batch, true, nullptr, path_for(batch), h.stream);
+    launch_head(*bx, batch, epi_args(h, nullptr, true));
+    tdt::SelectArgs sa{};
+    sa.V = h.V;
+    sa.ntile = h.ntile;
+    sa.partials = h.partials;
+    sa.rows = h.rows;
+    sa.tokens = tokens;
+    tdt::launch_select(h, batch, sa, h.stream);
+    return 1;
+    API_CATCH(0)
+}
+
+TURBO_DT_API int turbo_softcap(void* stream, float* z, size_t n, float cap) {
+    clear_error();
+    API_TRY
+    if (!z && n) throw std::runtime_error("z is NULL");
+    tdt::launch_softcap(z, n, cap, static_cast<hipStream_t>(stream));
+    return 1;
+    API_CATCH(0)
+}
+
+TURBO_DT_API int turbo_apply_repetition_penalty(void* stream, float* logits, uint32_t vocab,
+                                                const uint32_t* history, uint32_t n,
+                                                float penalty, float softcap) {
+    clear_error();
+    API_TRY
+    if (!logits || (n && !history)) throw std::runtime_error("logits or history is NULL");
+    tdt::launch_repetition(logits, vocab, history, n, penalty, softcap,
+                           static_cast<hipStream_t>(stream));
+    return 1;
+    API_CATCH(0)
+}
+
+TURBO_DT_API int turbo_lmhead_enable_head_timing(void* handle, int enable) {
+    clear_error();
+    API_TRY
+    HandleBox* bx = box(handle);
+    Head& h = bx->h;
+    check_hip(hipSetDevice(h.device), "hipSetDevice");
+    if (enable && !h.t_start[0]) {
+        for (int i = 0; i < Head::kTimerSlots; ++i) {
+            check_hip(hipEventCreate(&h.t_start[i]), "timer events");
+            check_hip(hipEventCreate(&h.t_stop[i]), "timer events");
+        }
+    }
+    h.timing = enable != 0;
+    return 1;
+    API_CATCH(0)
+}
+
+TURBO_DT_API int turbo_lmhead_head_kernel_time(void* handle, double* total_ms, int* launches,
+                                               int reset) {
+    clear_error();
+    API_TRY
+    HandleBox* bx = box(handle);
+    Head& h = bx->h;
+    check_hip(hipSetDevice(h.device), "hipSetDevice");
+    check_hip(hipStreamSynchronize(h.stream), "timer sync");
+    double ms = bx->t_accum_ms;
+    int n = bx->t_accum_n;
+    for (int i = 0; i < h.t_count; ++i) {
+        float e = 0.f;
+        check_hip(hipEventElapsedTime(&e, h.t_start[i], h.t_stop[i]), "timer read");
+        ms += e;
+    }
+    n += h.t_count;
+    if (total_ms) *total_ms = ms;
+    if (launches) *launches = n;
+    if (reset) {
+        bx->t_accum_ms = 0.0;
+        bx->t_accum_n = 0;
+        h.t_count = 0;
+    }
+    return 1;
+    API_CATCH(0)
+}
+
+}  // extern "C"

@@ -1,0 +1,70 @@
+// Fused epilogue of the head kernels: one wave64 holds 64 consecutive vocabulary ids of one
+// batch row. It applies, per id and in this order:
+//   softcap      30 * tanh(z / 30)                      src/cpu_reference.cpp:535-538
+//   logit bias   + summed bias                           (extension)
+//   repetition   per occurrence, clamp +-0.9999*softcap  src/sampling.cpp:74-90
+//   presence / frequency                                 (extension)
+//   ban          -> -inf                                 (extension)
+// then stores the logit (optional) and the block partial (max, lowest argmax, sum exp(l-max)).
+#pragma once
+
+#include "dt_internal.h"
+
+namespace tdt {
+
+__device__ inline float apply_entry(float l, const ModEntry& m, const DevRow& row, float limit) {
+    if (m.has_bias) l = __fadd_rn(l, m.bias);
+    if (m.count) {
+        const float p = row.repetition_penalty;
+        if (p != 1.0f) {
+            for (uint32_t c = 0; c < m.count; ++c) {
+                l = (l > 0.0f) ? __fdiv_rn(l, p) : __fmul_rn(l, p);
+                if (limit > 0.0f) l = fminf(fmaxf(l, -limit), limit);
+            }
+        }
+        if (row.presence_penalty != 0.0f || row.frequency_penalty != 0.0f) {
+            l = __fsub_rn(l, row.presence_penalty);
+            l = __fsub_rn(l, __fmul_rn(row.frequency_penalty, (float)m.count));
+        }
+    }
+    return l;
+}
+
+// acc: the raw head value of id = tile*64 + lane for batch row b (wave-uniform b and tile).
+__device__ inline void epilogue_wave(float acc, uint32_t b, uint32_t tile, uint32_t lane,
+                                     const EpiArgs& ep) {
+    const uint32_t id = tile * kTileRows + lane;
+    const bool valid = id < ep.V;
+    float l = acc;
+    if (ep.cap > 0.0f) l = __fmul_rn(ep.cap, tanhf(__fdiv_rn(l, ep.cap)));
+    const DevRow& row = ep.rows[b];
+    if (row.has_mods && ep.block_start) {
+        const uint32_t* bs = ep.block_start + (size_t)b * (ep.ntile + 1) + tile;
+        const uint32_t s = bs[0], e = bs[1];
+        const ModEntry* me = ep.mods + (size_t)b * ep.mod_cap;
+        for (uint32_t k = s; k < e; ++k) {
+            const ModEntry m = me[k];
+            if (m.id == id) l = apply_entry(l, m, row, ep.rep_limit);
+        }
+    }
+    if (ep.ban && valid) {
+        const uint32_t w = ep.ban[(size_t)b * ep.ban_stride + (id >> 5)];
+        if ((w >> (id & 31u)) & 1u) l = -INFINITY;
+    }
+    if (!valid) l = -INFINITY;
+    if (ep.logits && valid) ep.logits[(size_t)b * ep.V + id] = l;
+    const float m = wave_max(l);
+    const uint32_t arg = wave_min_u(l == m ? id : 0xFFFFFFFFu);
+    float se = (m == -INFINITY) ? 0.0f : __expf(l - m);
+    se = wave_sum(se);
+    if (lane == 0) {
+        BlockPartial bp;
+        bp.max = m;
+        bp.arg = arg;
+        bp.sumexp = se;
+        bp.pad = 0u;
+        ep.partials[(size_t)b * ep.ntile + tile] = bp;
+    }
+}
+
+}  // namespace tdt

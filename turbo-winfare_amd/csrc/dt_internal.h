@@ -1,0 +1,118 @@
+// Internal interfaces between the C-ABI layer (api.cpp) and the kernel files.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "dt_common.h"
+
+namespace tdt {
+
+// Device-resident head plus per-step scratch. All sizes are fixed at create time.
+struct Head {
+    int device = 0;
+    uint32_t V = 0;        // vocabulary rows
+    uint32_t D = 0;        // hidden size
+    uint32_t G = 0;        // groups per row (D / 64)
+    uint32_t NC = 0;       // 16-byte chunks per row (D / 32)
+    uint32_t ntile = 0;    // 64-row tiles (ceil(V / 64)); rows >= V are zero padding
+    float cap = 0.f;       // final-logit softcap (0 = off)
+    float eps = 0.f;
+    hipStream_t stream = nullptr;
+
+    // Tiled table: Wt[tile][chunk][64 rows] of 16 bytes, SBt[tile][group][64 rows] of
+    // (scale bf16 | bias bf16 << 16).
+    uint4* Wt = nullptr;
+    uint32_t* SBt = nullptr;
+    uint16_t* gamma = nullptr;   // [D] bf16 or null
+
+    int max_batch = 0;
+    uint32_t mod_cap = 0;        // max modifier entries per row (history + bias)
+
+    // Per-step scratch.
+    float* xn = nullptr;         // [max_batch][D] normalised activations
+    uint32_t* xdig = nullptr;    // [max_batch][NC][6][4] digit planes (small-batch GEMV)
+    float* xws = nullptr;        // [max_batch][G] block-fp scale 2^(e-21)
+    float* xsum = nullptr;       // [max_batch][G] sum of the block-fp activations
+    uint16_t* x16 = nullptr;     // [max_batch][D] fp16, k-permuted within octets (MFMA path)
+    float* logits = nullptr;     // [max_batch][V] scratch logits
+    BlockPartial* partials = nullptr;  // [max_batch][ntile]
+    DevRow* rows = nullptr;      // [max_batch]
+    ModEntry* mods = nullptr;    // [max_batch][mod_cap]
+    uint32_t* mod_count = nullptr;     // [max_batch]
+    uint32_t* block_start = nullptr;   // [max_batch][ntile + 1]
+    void* list_scratch = nullptr;      // [max_batch][V] uint2 compaction lists (select)
+
+    // Host staging ring for DevRow uploads (pinned).
+    static constexpr int kRing = 8;
+    DevRow* ring_host = nullptr;       // [kRing][max_batch]
+    hipEvent_t ring_ev[kRing] = {};
+    int ring_pos = 0;
+
+    // Head-kernel timing.
+    bool timing = false;
+    static constexpr int kTimerSlots = 1024;
+    hipEvent_t t_start[kTimerSlots] = {};
+    hipEvent_t t_stop[kTimerSlots] = {};
+    int t_count = 0;
+};
+
+// Arguments shared by the head-kernel epilogues and the logits-only epilogue.
+struct EpiArgs {
+    uint32_t V;
+    uint32_t ntile;
+    float cap;                 // softcap applied to the raw accumulator (0 = skip)
+    float* logits;             // [B][V] or null (not written)
+    BlockPartial* partials;    // [B][ntile]
+    const DevRow* rows;        // [B]
+    const ModEntry* mods;      // [B][mod_cap] or null
+    uint32_t mod_cap;
+    const uint32_t* block_start;  // [B][ntile + 1] or null
+    const uint32_t* ban;       // [B][ban_stride] or null
+    uint32_t ban_stride;
+    float rep_limit;           // 0.9999 * softcap used by the repetition clamp (0 = none)
+};
+
+enum class HeadPath { Digits, Mfma };
+
+// prep.cpp/hip
+void launch_repack(const Head& h, const uint8_t* W, const uint16_t* S, const uint16_t* B,
+                   hipStream_t st);
+void launch_prep(const Head& h, const void* hidden, int dtype, int batch, bool normed,
+                 float* xn_out, HeadPath path, hipStream_t st);
+void launch_modtable(const Head& h, int batch, const uint32_t* history, uint32_t hist_stride,
+                     const uint32_t* hist_len, const uint32_t* bias_ids, const float* bias_vals,
+                     uint32_t bias_stride, const uint32_t* bias_count, hipStream_t st);
+
+// gemv_digits.hip / gemm_mfma.hip
+void launch_head_digits(const Head& h, int batch, const EpiArgs& ep, hipStream_t st);
+void launch_head_mfma(const Head& h, int batch, const EpiArgs& ep, hipStream_t st);
+// epilogue over caller logits (no GEMV): logits are read, modified and summarised in place.
+void launch_logits_epilogue(const Head& h, int batch, const EpiArgs& ep, hipStream_t st);
+
+// select.hip
+struct SelectArgs {
+    uint32_t V;
+    uint32_t ntile;
+    const float* logits;          // [B][V] final logits (may be null for all-greedy)
+    const BlockPartial* partials; // [B][ntile]
+    const DevRow* rows;
+    const float* uniforms;        // [B] or null
+    uint32_t* tokens;
+    void* report;                 // TurboRowReport* or null
+    uint32_t* history;            // append target or null
+    uint32_t hist_stride;
+    uint32_t* hist_len;
+};
+void launch_select(const Head& h, int batch, const SelectArgs& a, hipStream_t st);
+
+// misc.hip
+void launch_softcap(float* z, size_t n, float cap, hipStream_t st);
+void launch_repetition(float* logits, uint32_t vocab, const uint32_t* history, uint32_t n,
+                       float penalty, float softcap, hipStream_t st);
+
+// Throws std::runtime_error with the HIP error string on failure.
+void check_hip(hipError_t e, const char* what);
+
+}  // namespace tdt

@@ -1,0 +1,131 @@
+// Small-batch (B <= 2) affine-int4 LM head: a bandwidth-bound streaming GEMV.
+//
+// Reference semantics: out[row] = sum_g s_g * sum_j q_j x_j + b_g * sum_j x_j
+// (src/cpu_reference.cpp:55-84; shaders/GemvInt4.hlsl + Common.hlsli:98-141).
+//
+// Design (gfx950):
+//  * One wave64 per 64-row tile, lane = row. The tiled layout makes each wave's load of one
+//    16-byte chunk a contiguous 1 KiB (64 lanes x global_load_dwordx4); a tile is one 88 KiB
+//    contiguous stream at D = 2816.
+//  * Activations are block floating point with 21-bit mantissas per 64-element group, split
+//    into six signed 4-bit digit planes. With q' = q - 8 (one XOR of the word with 0x88888888)
+//    every weight word needs six v_dot8_i32_i4 against wave-uniform digit words that live in
+//    SGPRs (scalar loads). Products are exact integers, so only the per-group scale-back and
+//    the fp32 group combination round:
+//        row += s * (D_g * 2^(e-21)) + (8 s + b) * S_g,   D_g = sum q'_j X_j,  S_g = sum X_j 2^(e-21)
+//  * Per-group scale/bias come from the tiled (s | b << 16) words, one coalesced dword per lane.
+//  * Loads are software-pipelined kPF groups ahead.
+#include "dt_epilogue.h"
+
+namespace tdt {
+
+constexpr int kDigitWaves = 4;
+constexpr int kPF = 4;
+
+template <int NB>
+__global__ __launch_bounds__(kDigitWaves * 64) void k_head_digits(
+    const uint4* __restrict__ Wt, const uint32_t* __restrict__ SBt, const uint32_t* __restrict__ xdig,
+    const float* __restrict__ xws, const float* __restrict__ xsum, uint32_t NC, uint32_t G, EpiArgs ep) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t tile = blockIdx.x * kDigitWaves + wave;
+    if (tile >= ep.ntile) return;  // wave-uniform
+    const uint4* wp = Wt + (size_t)tile * NC * kTileRows + lane;
+    const uint32_t* sbp = SBt + (size_t)tile * G * kTileRows + lane;
+
+    float acc[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[nb] = 0.0f;
+
+    uint4 wa[kPF], wb[kPF];
+    uint32_t sb[kPF];
+#pragma unroll
+    for (int p = 0; p < kPF; ++p) {
+        if ((uint32_t)p < G) {
+            wa[p] = wp[(size_t)(2 * p) * kTileRows];
+            wb[p] = wp[(size_t)(2 * p + 1) * kTileRows];
+            sb[p] = sbp[(size_t)p * kTileRows];
+        }
+    }
+
+    for (uint32_t g0 = 0; g0 < G; g0 += kPF) {
+#pragma unroll
+        for (int p = 0; p < kPF; ++p) {
+            const uint32_t g = g0 + p;
+            if (g < G) {
+                const uint4 A = wa[p], Bw = wb[p];
+                const uint32_t s = sb[p];
+                const uint32_t gn = g + kPF;
+                if (gn < G) {
+                    wa[p] = wp[(size_t)(2 * gn) * kTileRows];
+                    wb[p] = wp[(size_t)(2 * gn + 1) * kTileRows];
+                    sb[p] = sbp[(size_t)gn * kTileRows];
+                }
+                const uint32_t wq[8] = {A.x ^ 0x88888888u, A.y ^ 0x88888888u, A.z ^ 0x88888888u,
+                                        A.w ^ 0x88888888u, Bw.x ^ 0x88888888u, Bw.y ^ 0x88888888u,
+                                        Bw.z ^ 0x88888888u, Bw.w ^ 0x88888888u};
+                const float sf = bf16_to_f32(s & 0xFFFFu);
+                const float bf = bf16_to_f32(s >> 16);
+                const float c8 = fmaf(8.0f, sf, bf);
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) {
+                    const uint32_t* xd = xdig + ((size_t)nb * NC + 2u * g) * kDigitWordsPerChunk;
+                    int a[kDigits];
+#pragma unroll
+                    for (uint32_t k = 0; k < kDigits; ++k) a[k] = 0;
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                            for (uint32_t k = 0; k < kDigits; ++k)
+                                a[k] = __builtin_amdgcn_sdot8((int)wq[4 * h + i],
+                                                              (int)xd[h * kDigitWordsPerChunk + k * 4 + i],
+                                                              a[k], false);
+                        }
+                    }
+                    uint32_t Dg = (uint32_t)a[0];
+#pragma unroll
+                    for (uint32_t k = 1; k < kDigits; ++k) Dg += (uint32_t)a[k] << (4u * k);
+                    const float t = sf * xws[(size_t)nb * G + g];
+                    acc[nb] = fmaf((float)(int)Dg, t, acc[nb]);
+                    acc[nb] = fmaf(c8, xsum[(size_t)nb * G + g], acc[nb]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) epilogue_wave(acc[nb], (uint32_t)nb, tile, lane, ep);
+}
+
+void launch_head_digits(const Head& h, int batch, const EpiArgs& ep, hipStream_t st) {
+    const unsigned grid = (h.ntile + kDigitWaves - 1) / kDigitWaves;
+    if (batch == 1)
+        hipLaunchKernelGGL(k_head_digits<1>, dim3(grid), dim3(kDigitWaves * 64), 0, st, h.Wt,
+                           h.SBt, h.xdig, h.xws, h.xsum, h.NC, h.G, ep);
+    else if (batch == 2)
+        hipLaunchKernelGGL(k_head_digits<2>, dim3(grid), dim3(kDigitWaves * 64), 0, st, h.Wt,
+                           h.SBt, h.xdig, h.xws, h.xsum, h.NC, h.G, ep);
+    else
+        throw std::runtime_error("digit GEMV supports batch 1 or 2");
+    check_hip(hipGetLastError(), "head (digit GEMV)");
+}
+
+// Modifier epilogue over caller-provided logits (no softcap, no GEMV): one wave per 64 ids.
+__global__ __launch_bounds__(256) void k_logits_epilogue(EpiArgs ep, const float* __restrict__ in) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t tile = blockIdx.x * 4 + wave;
+    const uint32_t b = blockIdx.y;
+    if (tile >= ep.ntile) return;
+    const uint32_t id = tile * kTileRows + lane;
+    const float v = (id < ep.V) ? in[(size_t)b * ep.V + id] : -INFINITY;
+    epilogue_wave(v, b, tile, lane, ep);
+}
+
+void launch_logits_epilogue(const Head& h, int batch, const EpiArgs& ep, hipStream_t st) {
+    const unsigned gx = (h.ntile + 3) / 4;
+    hipLaunchKernelGGL(k_logits_epilogue, dim3(gx, (unsigned)batch), dim3(256), 0, st, ep,
+                       (const float*)ep.logits);
+    check_hip(hipGetLastError(), "logits epilogue");
+}
+
+}  // namespace tdt

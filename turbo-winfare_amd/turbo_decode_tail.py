@@ -1,0 +1,315 @@
+"""ctypes binding of libturbo_decode_tail.so (include/turbo_decode_tail.h).
+
+The library is the product; this module only mirrors its C ABI for Python callers (tests,
+bench). Device buffers are passed as raw pointers (``tensor.data_ptr()`` of torch CUDA tensors
+works); torch is not required by this module.
+
+Loading fails loudly when the library has not been built: there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libturbo_decode_tail.so"
+
+TURBO_RNG_PHILOX = 0
+TURBO_RNG_REFERENCE = 1
+TURBO_ROW_FULL_VOCAB = 1
+TURBO_HIDDEN_F32 = 0
+TURBO_HIDDEN_BF16 = 1
+TURBO_STEP_NORMED = 1
+TURBO_STEP_APPEND_HISTORY = 2
+
+# Every symbol include/turbo_decode_tail.h declares.
+EXPORTS = (
+    "turbo_lmhead_last_error",
+    "turbo_lmhead_desc_default",
+    "turbo_lmhead_create",
+    "turbo_lmhead_destroy",
+    "turbo_lmhead_set_stream",
+    "turbo_lmhead_synchronize",
+    "turbo_lmhead_limits",
+    "turbo_sampling_row_default",
+    "turbo_validate_sampling",
+    "turbo_splitmix64",
+    "turbo_seed_for",
+    "turbo_row_uniform",
+    "turbo_lmhead_step",
+    "turbo_lmhead_rms_norm",
+    "turbo_lmhead_logits",
+    "turbo_lmhead_greedy",
+    "turbo_softcap",
+    "turbo_apply_repetition_penalty",
+    "turbo_sample_logits",
+    "turbo_lmhead_enable_head_timing",
+    "turbo_lmhead_head_kernel_time",
+)
+
+
+class TurboLMHeadDesc(C.Structure):
+    _fields_ = [
+        ("vocab_size", C.c_uint32),
+        ("hidden_size", C.c_uint32),
+        ("group_size", C.c_uint32),
+        ("final_logit_softcap", C.c_float),
+        ("rms_norm_eps", C.c_float),
+        ("weights_on_device", C.c_int),
+        ("weight", C.c_void_p),
+        ("scales", C.c_void_p),
+        ("biases", C.c_void_p),
+        ("norm_weight", C.c_void_p),
+        ("device", C.c_int),
+    ]
+
+
+class TurboSamplingRow(C.Structure):
+    _fields_ = [
+        ("temperature", C.c_float),
+        ("top_p", C.c_float),
+        ("top_k", C.c_int),
+        ("repetition_penalty", C.c_float),
+        ("presence_penalty", C.c_float),
+        ("frequency_penalty", C.c_float),
+        ("rng", C.c_int),
+        ("has_seed", C.c_int),
+        ("seed", C.c_uint64),
+        ("counter", C.c_uint64),
+        ("flags", C.c_uint32),
+    ]
+
+
+class TurboStepInputs(C.Structure):
+    _fields_ = [
+        ("batch", C.c_int),
+        ("hidden", C.c_void_p),
+        ("hidden_dtype", C.c_int),
+        ("flags", C.c_uint32),
+        ("rows", C.POINTER(TurboSamplingRow)),
+        ("history", C.c_void_p),
+        ("history_stride", C.c_uint32),
+        ("history_len", C.c_void_p),
+        ("ban_bits", C.c_void_p),
+        ("ban_stride", C.c_uint32),
+        ("bias_ids", C.c_void_p),
+        ("bias_values", C.c_void_p),
+        ("bias_stride", C.c_uint32),
+        ("bias_count", C.c_void_p),
+        ("uniforms", C.c_void_p),
+    ]
+
+
+class TurboRowReport(C.Structure):
+    _fields_ = [
+        ("max_logit", C.c_float),
+        ("u", C.c_float),
+        ("shortlist", C.c_uint32),
+        ("cut", C.c_uint32),
+        ("rank", C.c_uint32),
+        ("path", C.c_uint32),
+        ("total", C.c_double),
+        ("denom", C.c_double),
+        ("r", C.c_double),
+    ]
+
+
+class TurboStepOutputs(C.Structure):
+    _fields_ = [
+        ("tokens", C.c_void_p),
+        ("logits", C.c_void_p),
+        ("report", C.c_void_p),
+    ]
+
+
+_lib = None
+
+
+def load(path: os.PathLike | str | None = None) -> C.CDLL:
+    """Loads the built library (raises if it is missing)."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise FileNotFoundError(
+            f"{p} is missing: build it with `python turbo-winfare_amd/build.py` "
+            "(there is no fallback implementation)")
+    lib = C.CDLL(str(p))
+    vp, u32, i32, f32 = C.c_void_p, C.c_uint32, C.c_int, C.c_float
+    sig = {
+        "turbo_lmhead_last_error": (C.c_char_p, []),
+        "turbo_lmhead_desc_default": (None, [C.POINTER(TurboLMHeadDesc)]),
+        "turbo_lmhead_create": (vp, [C.POINTER(TurboLMHeadDesc)]),
+        "turbo_lmhead_destroy": (None, [vp]),
+        "turbo_lmhead_set_stream": (i32, [vp, vp]),
+        "turbo_lmhead_synchronize": (i32, [vp]),
+        "turbo_lmhead_limits": (i32, [vp, C.POINTER(i32), C.POINTER(i32)]),
+        "turbo_sampling_row_default": (None, [C.POINTER(TurboSamplingRow)]),
+        "turbo_validate_sampling": (i32, [C.POINTER(TurboSamplingRow)]),
+        "turbo_splitmix64": (C.c_uint64, [C.c_uint64]),
+        "turbo_seed_for": (C.c_uint64, [i32, C.c_uint64, i32]),
+        "turbo_row_uniform": (f32, [C.POINTER(TurboSamplingRow)]),
+        "turbo_lmhead_step": (i32, [vp, C.POINTER(TurboStepInputs), C.POINTER(TurboStepOutputs)]),
+        "turbo_lmhead_rms_norm": (i32, [vp, vp, i32, vp]),
+        "turbo_lmhead_logits": (i32, [vp, vp, i32, i32, i32, vp]),
+        "turbo_lmhead_greedy": (i32, [vp, vp, i32, i32, vp]),
+        "turbo_softcap": (i32, [vp, vp, C.c_size_t, f32]),
+        "turbo_apply_repetition_penalty": (i32, [vp, vp, u32, vp, u32, f32, f32]),
+        "turbo_sample_logits": (i32, [vp, vp, C.POINTER(TurboStepInputs), C.POINTER(TurboStepOutputs)]),
+        "turbo_lmhead_enable_head_timing": (i32, [vp, i32]),
+        "turbo_lmhead_head_kernel_time": (i32, [vp, C.POINTER(C.c_double), C.POINTER(i32), i32]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    return load().turbo_lmhead_last_error().decode()
+
+
+class TurboError(RuntimeError):
+    pass
+
+
+def _ok(rc: int) -> None:
+    if not rc:
+        raise TurboError(last_error())
+
+
+def row_default(**kw) -> TurboSamplingRow:
+    r = TurboSamplingRow()
+    load().turbo_sampling_row_default(C.byref(r))
+    for k, v in kw.items():
+        setattr(r, k, v)
+    return r
+
+
+def validate(row: TurboSamplingRow) -> tuple[bool, str]:
+    ok = bool(load().turbo_validate_sampling(C.byref(row)))
+    return ok, ("" if ok else last_error())
+
+
+def row_uniform(row: TurboSamplingRow) -> float:
+    return float(load().turbo_row_uniform(C.byref(row)))
+
+
+def _ptr(t) -> int | None:
+    if t is None:
+        return None
+    return int(t.data_ptr()) if hasattr(t, "data_ptr") else int(t)
+
+
+class LMHead:
+    """Owns one turbo_lmhead handle. Arrays: numpy (host) or torch CUDA tensors (device)."""
+
+    def __init__(self, weight, scales, biases, norm_weight=None, *, vocab: int, hidden: int,
+                 softcap: float = 30.0, eps: float = 1e-6, on_device: bool = False, device: int = 0):
+        self.lib = load()
+        d = TurboLMHeadDesc()
+        self.lib.turbo_lmhead_desc_default(C.byref(d))
+        d.vocab_size = vocab
+        d.hidden_size = hidden
+        d.final_logit_softcap = softcap
+        d.rms_norm_eps = eps
+        d.weights_on_device = 1 if on_device else 0
+        d.device = device
+
+        def hp(a):
+            if a is None:
+                return None
+            if on_device:
+                return _ptr(a)
+            return a.ctypes.data
+
+        d.weight, d.scales, d.biases, d.norm_weight = hp(weight), hp(scales), hp(biases), hp(norm_weight)
+        self.vocab, self.hidden = vocab, hidden
+        h = self.lib.turbo_lmhead_create(C.byref(d))
+        if not h:
+            raise TurboError(last_error())
+        self.h = h
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            self.lib.turbo_lmhead_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def sync(self) -> None:
+        _ok(self.lib.turbo_lmhead_synchronize(self.h))
+
+    def limits(self) -> tuple[int, int]:
+        mb, mm = C.c_int(), C.c_int()
+        _ok(self.lib.turbo_lmhead_limits(self.h, C.byref(mb), C.byref(mm)))
+        return mb.value, mm.value
+
+    def rms_norm(self, x, batch: int, out) -> None:
+        _ok(self.lib.turbo_lmhead_rms_norm(self.h, _ptr(x), batch, _ptr(out)))
+
+    def logits(self, x, batch: int, out, *, dtype: int = TURBO_HIDDEN_F32, softcap: bool = True) -> None:
+        _ok(self.lib.turbo_lmhead_logits(self.h, _ptr(x), dtype, batch, 1 if softcap else 0, _ptr(out)))
+
+    def greedy(self, x, batch: int, tokens, *, dtype: int = TURBO_HIDDEN_F32) -> None:
+        _ok(self.lib.turbo_lmhead_greedy(self.h, _ptr(x), dtype, batch, _ptr(tokens)))
+
+    @staticmethod
+    def make_inputs(batch, rows, *, hidden=None, dtype=TURBO_HIDDEN_F32, flags=0, history=None,
+                    history_len=None, ban=None, bias_ids=None, bias_values=None, bias_count=None,
+                    uniforms=None):
+        arr = (TurboSamplingRow * batch)(*rows)
+        inp = TurboStepInputs()
+        inp.batch = batch
+        inp.hidden = _ptr(hidden)
+        inp.hidden_dtype = dtype
+        inp.flags = flags
+        inp.rows = C.cast(arr, C.POINTER(TurboSamplingRow))
+        if history is not None:
+            inp.history = _ptr(history)
+            inp.history_stride = int(history.shape[1])
+            inp.history_len = _ptr(history_len)
+        if ban is not None:
+            inp.ban_bits = _ptr(ban)
+            inp.ban_stride = int(ban.shape[1])
+        if bias_ids is not None:
+            inp.bias_ids = _ptr(bias_ids)
+            inp.bias_values = _ptr(bias_values)
+            inp.bias_stride = int(bias_ids.shape[1])
+            inp.bias_count = _ptr(bias_count)
+        inp.uniforms = _ptr(uniforms)
+        return inp, arr  # keep arr alive with the struct
+
+    def step(self, inp: TurboStepInputs, tokens, logits=None, report=None) -> None:
+        out = TurboStepOutputs(_ptr(tokens), _ptr(logits), _ptr(report))
+        _ok(self.lib.turbo_lmhead_step(self.h, C.byref(inp), C.byref(out)))
+
+    def sample_logits(self, logits, inp: TurboStepInputs, tokens, report=None) -> None:
+        out = TurboStepOutputs(_ptr(tokens), None, _ptr(report))
+        _ok(self.lib.turbo_sample_logits(self.h, _ptr(logits), C.byref(inp), C.byref(out)))
+
+    def enable_head_timing(self, on: bool = True) -> None:
+        _ok(self.lib.turbo_lmhead_enable_head_timing(self.h, 1 if on else 0))
+
+    def head_kernel_time(self, reset: bool = False) -> tuple[float, int]:
+        ms, n = C.c_double(), C.c_int()
+        _ok(self.lib.turbo_lmhead_head_kernel_time(self.h, C.byref(ms), C.byref(n), 1 if reset else 0))
+        return ms.value, n.value
+
+
+def softcap(z, n: int, cap: float, stream=None) -> None:
+    _ok(load().turbo_softcap(stream, _ptr(z), n, cap))
+
+
+def apply_repetition_penalty(logits, vocab: int, history, n: int, penalty: float, softcap: float,
+                             stream=None) -> None:
+    _ok(load().turbo_apply_repetition_penalty(stream, _ptr(logits), vocab, _ptr(history), n,
+                                              penalty, softcap))
