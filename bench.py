@@ -53,6 +53,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-batches", action="store_true")
     ap.add_argument("--cpu-steps", type=int, default=4)
+    ap.add_argument("--only", choices=["b1", "b32", "b256"], default=None,
+                    help="run one workload only (profiling); prints its own JSON line")
     return ap.parse_args()
 
 
@@ -186,6 +188,12 @@ def main():
     W, S, B, g = synth.make_head(V, D, SEED)
     head = T.LMHead(W, S, B, g, vocab=V, hidden=D)
     head.enable_head_timing(True)
+    if a.only in ("b32", "b256"):
+        B = 32 if a.only == "b32" else 256
+        res = batched_line(T, torch, head, B, a.warmup, a.steps)
+        head.close()
+        print(json.dumps({"only": a.only, **res}), flush=True)
+        return
     total = a.warmup + a.steps
     c2 = Config2(T, torch, head, total)
     log(f"warmup {a.warmup} steps")
@@ -224,12 +232,12 @@ def main():
                      "kernel": "k_head_digits<1>", "kernel_avg_us": 1e3 * kavg_ms,
                      "algorithmic_bytes_per_launch": bytes_per_launch},
     }
-    if not a.no_batches:
+    if not a.no_batches and a.only is None:
         log("batched lines")
         line["batches"] = {"B32": batched_line(T, torch, head, 32, 5, 50),
                            "B256": batched_line(T, torch, head, 256, 3, 20)}
     head.close()
-    if not a.no_cpu:
+    if not a.no_cpu and a.only is None:
         log("cpu baseline")
         line["cpu_baseline"] = cpu_baseline(W, S, B, g, a.cpu_steps)
     print(json.dumps(line), flush=True)

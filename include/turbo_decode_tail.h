@@ -165,7 +165,8 @@ typedef struct {
     uint32_t shortlist;     /* candidate list size (want) */
     uint32_t cut;           /* survivors after top-p / top-k */
     uint32_t rank;          /* token's position among the survivors */
-    uint32_t path;          /* 0 greedy, 1 shortlist, 2 full-vocabulary radix, 3 degenerate */
+    uint32_t path;          /* 0 greedy, 1 shortlist, 2 full-vocabulary value bins,
+                               3 degenerate, 4 radix fallback (massive ties) */
     double total;           /* sum exp(l - max) over the row */
     double denom;           /* survivor weight sum */
     double r;               /* u * denom */

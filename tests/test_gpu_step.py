@@ -229,3 +229,12 @@ def test_sampler_paths(head, kind):
     assert np.array_equal(after, base)  # no modifiers requested: logits untouched
     us = [T.row_uniform(r) for r in rows]
     check_sampler_on_gpu_logits(rows, toks, base, us)
+    paths = rep.view(np.uint32)[:, 5]  # TurboRowReport.path
+    for i, (t, p, k, f) in enumerate(cfgs):
+        if t <= 0:
+            assert paths[i] == 0
+        elif f and k == 0:
+            # full vocabulary: value bins, or the radix fallback when a bin is a massive tie
+            assert paths[i] == 2 or (kind == "ties" and paths[i] == 4), (i, paths[i])
+        elif kind != "ties":
+            assert paths[i] == 1, (i, paths[i])

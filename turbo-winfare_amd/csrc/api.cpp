@@ -163,17 +163,58 @@ void free_head(Head& h) {
     }
 }
 
-// Copies B DevRows through the pinned ring onto the device row buffer (stream-ordered).
-void upload_rows(Head& h, const tdt::DevRow* rows, int B) {
+// Stages B DevRows in the next slot of the pinned ring and returns the slot's device-visible
+// address. The step-prep kernel copies the slot into device memory, so no separate copy is
+// enqueued; the slot is reused only after the event recorded behind that kernel has passed.
+const tdt::DevRow* stage_rows(Head& h, const tdt::DevRow* rows, int B, int* pos_out) {
     const int pos = h.ring_pos;
     h.ring_pos = (h.ring_pos + 1) % Head::kRing;
     check_hip(hipEventSynchronize(h.ring_ev[pos]), "row staging wait");
     tdt::DevRow* slot = h.ring_host + static_cast<size_t>(pos) * h.max_batch;
     std::memcpy(slot, rows, sizeof(tdt::DevRow) * B);
-    check_hip(hipMemcpyAsync(h.rows, slot, sizeof(tdt::DevRow) * B, hipMemcpyHostToDevice,
-                             h.stream),
-              "row upload");
+    *pos_out = pos;
+    return h.ring_dev + static_cast<size_t>(pos) * h.max_batch;
+}
+
+void release_slot(Head& h, int pos) {
     check_hip(hipEventRecord(h.ring_ev[pos], h.stream), "row staging record");
+}
+
+tdt::PrepArgs prep_args(const Head& h, const tdt::DevRow* src, int B) {
+    tdt::PrepArgs a{};
+    a.B = B;
+    a.rows_src = src;
+    a.rows_dst = h.rows;
+    a.gamma = h.gamma;
+    a.eps = h.eps;
+    a.D = h.D;
+    a.xdig = h.xdig;
+    a.xws = h.xws;
+    a.xsum = h.xsum;
+    a.x16 = h.x16;
+    a.V = h.V;
+    a.ntile = h.ntile;
+    a.P = 2;
+    a.mods = h.mods;
+    a.mod_cap = h.mod_cap;
+    a.mod_count = h.mod_count;
+    a.block_start = h.block_start;
+    return a;
+}
+
+// Row parameters + (optionally) activations, no modifiers: one step-prep launch.
+void simple_prep(Head& h, const tdt::DevRow* rows, int B, const void* x, int dtype, bool normed,
+                 float* xn, tdt::HeadPath path) {
+    int pos = 0;
+    const tdt::DevRow* src = stage_rows(h, rows, B, &pos);
+    tdt::PrepArgs a = prep_args(h, src, B);
+    a.hidden = x;
+    a.dtype = dtype;
+    a.normed = normed ? 1 : 0;
+    a.xn = xn;
+    a.path = path == tdt::HeadPath::Digits ? 0 : 1;
+    tdt::launch_step_prep(h, a, false, h.stream);
+    release_slot(h, pos);
 }
 
 tdt::DevRow make_devrow(const Head& h, const TurboSamplingRow& r, uint32_t has_mods) {
@@ -276,22 +317,32 @@ int run_rows(HandleBox& bx, const TurboStepInputs* in, const TurboStepOutputs* o
         all_greedy = all_greedy && r.temperature <= 0.0f;
         rows[b] = make_devrow(h, r, mods);
     }
-    if (any_mods) {
-        const uint32_t n = (has_hist ? in->history_stride : 0u) + (has_bias ? in->bias_stride : 0u);
-        if (n > h.mod_cap)
-            throw std::runtime_error("history_stride + bias_stride exceeds " + std::to_string(h.mod_cap));
-    }
-    upload_rows(h, rows, B);
-
-    float* logits = given_logits ? given_logits : (out->logits ? out->logits : (all_greedy ? nullptr : h.logits));
-    if (hidden) {
-        tdt::launch_prep(h, hidden, in->hidden_dtype, B, (in->flags & TURBO_STEP_NORMED) != 0,
-                         nullptr, path_for(B), h.stream);
-    }
+    uint32_t P = 2;
     if (any_mods)
-        tdt::launch_modtable(h, B, has_hist ? in->history : nullptr, in->history_stride,
-                             in->history_len, has_bias ? in->bias_ids : nullptr, in->bias_values,
-                             in->bias_stride, in->bias_count, h.stream);
+        P = tdt::modtable_sort_size(h, (has_hist ? in->history_stride : 0u) + (has_bias ? in->bias_stride : 0u));
+    float* logits = given_logits ? given_logits : (out->logits ? out->logits : (all_greedy ? nullptr : h.logits));
+
+    int pos = 0;
+    const tdt::DevRow* src = stage_rows(h, rows, B, &pos);
+    tdt::PrepArgs pa = prep_args(h, src, B);
+    pa.hidden = hidden;
+    pa.dtype = in->hidden_dtype == TURBO_HIDDEN_BF16 ? 1 : 0;
+    pa.normed = (in->flags & TURBO_STEP_NORMED) ? 1 : 0;
+    pa.path = path_for(B) == tdt::HeadPath::Digits ? 0 : 1;
+    pa.P = P;
+    if (has_hist) {
+        pa.history = in->history;
+        pa.hist_stride = in->history_stride;
+        pa.hist_len = in->history_len;
+    }
+    if (has_bias) {
+        pa.bias_ids = in->bias_ids;
+        pa.bias_vals = in->bias_values;
+        pa.bias_stride = in->bias_stride;
+        pa.bias_count = in->bias_count;
+    }
+    tdt::launch_step_prep(h, pa, any_mods, h.stream);
+    release_slot(h, pos);
     tdt::EpiArgs ep = epi_args(h, logits, hidden != nullptr);
     ep.ban = in->ban_bits;
     ep.ban_stride = in->ban_stride;
@@ -426,8 +477,11 @@ TURBO_DT_API void* turbo_lmhead_create(const TurboLMHeadDesc* d) {
         h.block_start = dalloc<uint32_t>(MB * (h.ntile + 1u), "alloc block_start");
         h.list_scratch = dalloc<uint2>(MB * h.V, "alloc list scratch");
         check_hip(hipHostMalloc(reinterpret_cast<void**>(&h.ring_host),
-                                sizeof(tdt::DevRow) * MB * Head::kRing, hipHostMallocDefault),
+                                sizeof(tdt::DevRow) * MB * Head::kRing,
+                                hipHostMallocMapped | hipHostMallocCoherent),
                   "alloc pinned ring");
+        check_hip(hipHostGetDevicePointer(reinterpret_cast<void**>(&h.ring_dev), h.ring_host, 0),
+                  "map pinned ring");
         for (int i = 0; i < Head::kRing; ++i)
             check_hip(hipEventCreateWithFlags(&h.ring_ev[i], hipEventDisableTiming), "ring events");
         check_hip(hipDeviceSynchronize(), "create");
@@ -545,7 +599,9 @@ TURBO_DT_API int turbo_lmhead_rms_norm(void* handle, const float* x, int batch, 
     check_hip(hipSetDevice(h.device), "hipSetDevice");
     check_batch(h, batch);
     if (!x || !out) throw std::runtime_error("x or out is NULL");
-    tdt::launch_prep(h, x, TURBO_HIDDEN_F32, batch, false, out, tdt::HeadPath::Digits, h.stream);
+    tdt::DevRow rows[kMaxBatch];
+    for (int b = 0; b < batch; ++b) rows[b] = greedy_devrow(h);
+    simple_prep(h, rows, batch, x, 0, false, out, tdt::HeadPath::Digits);
     return 1;
     API_CATCH(0)
 }
@@ -563,8 +619,7 @@ TURBO_DT_API int turbo_lmhead_logits(void* handle, const void* x, int x_dtype, i
         throw std::runtime_error("x_dtype must be TURBO_HIDDEN_F32 or TURBO_HIDDEN_BF16");
     tdt::DevRow rows[kMaxBatch];
     for (int b = 0; b < batch; ++b) rows[b] = greedy_devrow(h);
-    upload_rows(h, rows, batch);
-    tdt::launch_prep(h, x, x_dtype, batch, true, nullptr, path_for(batch), h.stream);
+    simple_prep(h, rows, batch, x, x_dtype == TURBO_HIDDEN_BF16 ? 1 : 0, true, nullptr, path_for(batch));
     launch_head(*bx, batch, epi_args(h, logits, apply_softcap != 0));
     return 1;
     API_CATCH(0)
@@ -583,8 +638,7 @@ TURBO_DT_API int turbo_lmhead_greedy(void* handle, const void* x, int x_dtype, i
         throw std::runtime_error("x_dtype must be TURBO_HIDDEN_F32 or TURBO_HIDDEN_BF16");
     tdt::DevRow rows[kMaxBatch];
     for (int b = 0; b < batch; ++b) rows[b] = greedy_devrow(h);
-    upload_rows(h, rows, batch);
-    tdt::launch_prep(h, x, x_dtype, batch, true, nullptr, path_for(batch), h.stream);
+    simple_prep(h, rows, batch, x, x_dtype == TURBO_HIDDEN_BF16 ? 1 : 0, true, nullptr, path_for(batch));
     launch_head(*bx, batch, epi_args(h, nullptr, true));
     tdt::SelectArgs sa{};
     sa.V = h.V;

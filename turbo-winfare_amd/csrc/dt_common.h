@@ -18,7 +18,7 @@ struct BlockPartial {
     float max;       // block maximum after modifiers (-inf when every id is banned)
     uint32_t arg;    // lowest id holding the maximum
     float sumexp;    // sum exp(l - max) over the block (0 when max is -inf)
-    uint32_t pad;
+    float minf;      // smallest finite logit of the block (+inf when none)
 };
 
 // One sorted modifier entry (per row, unique id).
@@ -86,6 +86,11 @@ __host__ __device__ inline uint32_t philox4x32_10_x(uint64_t counter, uint64_t s
 __device__ inline float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ inline float wave_min(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o, 64));
     return v;
 }
 __device__ inline float wave_sum(float v) {

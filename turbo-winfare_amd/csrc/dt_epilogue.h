@@ -57,12 +57,13 @@ __device__ inline void epilogue_wave(float acc, uint32_t b, uint32_t tile, uint3
     const uint32_t arg = wave_min_u(l == m ? id : 0xFFFFFFFFu);
     float se = (m == -INFINITY) ? 0.0f : __expf(l - m);
     se = wave_sum(se);
+    const float mn = wave_min(l == -INFINITY ? INFINITY : l);
     if (lane == 0) {
         BlockPartial bp;
         bp.max = m;
         bp.arg = arg;
         bp.sumexp = se;
-        bp.pad = 0u;
+        bp.minf = mn;
         ep.partials[(size_t)b * ep.ntile + tile] = bp;
     }
 }

@@ -46,7 +46,8 @@ struct Head {
 
     // Host staging ring for DevRow uploads (pinned).
     static constexpr int kRing = 8;
-    DevRow* ring_host = nullptr;       // [kRing][max_batch]
+    DevRow* ring_host = nullptr;       // [kRing][max_batch], pinned, mapped, coherent
+    DevRow* ring_dev = nullptr;        // device-visible address of ring_host
     hipEvent_t ring_ev[kRing] = {};
     int ring_pos = 0;
 
@@ -76,14 +77,42 @@ struct EpiArgs {
 
 enum class HeadPath { Digits, Mfma };
 
-// prep.cpp/hip
+// prep.hip
+struct PrepArgs {
+    int B;
+    const DevRow* rows_src;      // host-mapped staging slot (or device memory)
+    DevRow* rows_dst;            // device row buffer, filled by block 0 (null: skip the copy)
+    // activations (null hidden: no activation work)
+    const void* hidden;
+    int dtype;                   // 0 fp32, 1 bf16
+    int normed;
+    const uint16_t* gamma;
+    float eps;
+    uint32_t D;
+    float* xn;                   // optional normalised copy [B][D]
+    int path;                    // 0 digit planes, 1 fp16
+    uint32_t* xdig;
+    float* xws;
+    float* xsum;
+    uint16_t* x16;
+    // modifier table
+    uint32_t V, ntile, P;
+    const uint32_t* history;
+    uint32_t hist_stride;
+    const uint32_t* hist_len;
+    const uint32_t* bias_ids;
+    const float* bias_vals;
+    uint32_t bias_stride;
+    const uint32_t* bias_count;
+    ModEntry* mods;
+    uint32_t mod_cap;
+    uint32_t* mod_count;
+    uint32_t* block_start;
+};
 void launch_repack(const Head& h, const uint8_t* W, const uint16_t* S, const uint16_t* B,
                    hipStream_t st);
-void launch_prep(const Head& h, const void* hidden, int dtype, int batch, bool normed,
-                 float* xn_out, HeadPath path, hipStream_t st);
-void launch_modtable(const Head& h, int batch, const uint32_t* history, uint32_t hist_stride,
-                     const uint32_t* hist_len, const uint32_t* bias_ids, const float* bias_vals,
-                     uint32_t bias_stride, const uint32_t* bias_count, hipStream_t st);
+void launch_step_prep(const Head& h, const PrepArgs& a, bool with_mods, hipStream_t st);
+uint32_t modtable_sort_size(const Head& h, uint32_t n);
 
 // gemv_digits.hip / gemm_mfma.hip
 void launch_head_digits(const Head& h, int batch, const EpiArgs& ep, hipStream_t st);

@@ -1,23 +1,29 @@
 // Token selection: greedy argmax or the sampled draw of sample_token (src/sampling.cpp:92-169).
 //
 // One 1024-thread workgroup per batch row, reading the row's final logits and the per-64-id
-// block partials the head epilogue wrote (max, lowest argmax, sum exp(l - max)).
+// block partials the head epilogue wrote (max, lowest argmax, sum exp(l - max), finite min).
 //
 //  greedy     argmax of the block partials, ties to the lowest id (:97-104).
 //  shortlist  (want = top_k, or 256 without the full-vocabulary flag; :122-137)
-//             tau = want-th largest block maximum (count radix select over the partials) is a
-//             lower bound of the want-th largest logit, so every shortlist member lies in a
-//             block whose maximum is >= tau. Those blocks are gathered (elements >= tau),
+//             tau = lower edge of the 22-bit key bin holding the want-th largest block maximum
+//             is a lower bound of the want-th largest logit, so every shortlist member lies in
+//             a block whose maximum is >= tau. Those blocks are gathered (elements >= tau),
 //             bitonic-sorted by (logit desc, id asc), and the first `want` form the shortlist.
 //             Nucleus over full-distribution probabilities (:139-151) and the temperature draw
 //             (:153-168) run as double-precision block scans over <= 256 candidates.
-//  general    full-vocabulary nucleus (want = V) and shortlist overflow (more than kCandCap
-//             elements >= tau, e.g. massive ties): weighted radix select over the whole row.
-//             Each "find" locates the first element, in (logit desc, id asc) order within a
-//             prefix set, at which a cumulative weight reaches a target: an 11-bit histogram
-//             pass over the row, compaction of the crossing bucket, two more radix levels on
-//             the compacted list, then the tie among equal keys (equal weights) is resolved
-//             by count and a radix select over ids.
+//  full vocabulary (top_k = 0 with the full-vocabulary flag; the full-sort sampler of
+//             tests/test_sampling.cpp:36-84): one pass builds 2048-bin histograms of both the
+//             T = 1 and the temperature weights over equal-width logit-value bins spanning
+//             [lo, max] (bin order is rank order). The nucleus bin and the bins the draw can
+//             land in (bounded before the cut is known) are gathered in a second pass,
+//             bitonic-sorted, and resolved with double-precision scans.
+//  fallback   shortlist overflow or a bin too large to gather (massive ties): weighted radix
+//             select over the order-preserving keys, with ties among equal keys (equal
+//             weights) resolved by count and a radix select over ids.
+//
+// Weight histograms accumulate in LDS as u64 fixed point (w * 2^40, weights relative to the
+// row maximum are <= 1): integer LDS atomics run an order of magnitude faster than float ones
+// on gfx950. Truncation changes a row total by at most V * 2^-40 relative.
 #include <stdexcept>
 
 #include "dt_internal.h"
@@ -26,9 +32,13 @@ namespace tdt {
 
 constexpr uint32_t kSelThreads = 1024;
 constexpr uint32_t kSelWaves = kSelThreads / 64;
-constexpr uint32_t kCandCap = 4096;
+constexpr uint32_t kCandCap = 8192;
 constexpr uint32_t kTileCap = 2048;
 constexpr uint32_t kBins = 2048;
+constexpr uint32_t kVBins = 2048;
+constexpr uint32_t kKeyCache = 8192;  // block-maximum keys kept in LDS (ntile <= 8192)
+constexpr int kInflight = 4;          // float4 loads in flight per thread in row passes
+constexpr double kFx = 1099511627776.0;  // 2^40: fixed-point scale of histogram weights
 
 // Must match TurboRowReport in include/turbo_decode_tail.h.
 struct RowReport {
@@ -45,19 +55,23 @@ struct RowReport {
 
 struct SelShared {
     union {
-        double hd[kBins];
+        unsigned long long hd[kBins];  // key-bin weights, fixed point
         uint32_t hu[kBins];
+        struct {
+            unsigned long long vm[kVBins];  // value-bin weights, T = 1, fixed point
+            unsigned long long vq[kVBins];  // value-bin weights, temperature T, fixed point
+        };
     };
     unsigned long long cand[kCandCap];
     uint32_t tiles[kTileCap];
+    uint32_t pkey[kKeyCache];
     double wsum_d[kSelWaves];
     uint32_t wsum_u[kSelWaves];
     float wmax[kSelWaves];
     uint32_t warg[kSelWaves];
-    // broadcast slots
+    float wmin[kSelWaves];
     double bd[4];
     uint32_t bu[8];
-    float bf[4];
 };
 
 // ---- block primitives ------------------------------------------------------------------------
@@ -81,7 +95,7 @@ __device__ inline uint32_t* wslot<uint32_t>(SelShared& s) { return s.wsum_u; }
 
 // Exclusive scan over the block in thread order; returns the exclusive prefix, total in *tot.
 template <typename T>
-__device__ inline T block_excl_scan(T v, SelShared& s, T* tot) {
+__device__ __attribute__((always_inline)) inline T block_excl_scan(T v, SelShared& s, T* tot) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const T incl = wave_incl_scan(v, lane);
     T* ws = wslot<T>(s);
@@ -118,18 +132,23 @@ __device__ inline uint32_t block_min_u(uint32_t v, SelShared& s) {
     return r;
 }
 
-// Finds, scanning the histogram from the highest bin down, the bin where the running total
-// first reaches `target` (before < target <= before + h). Returns 1 and sets bin/above when
-// target <= total. Otherwise returns 0, or with `clamp` uses target = total (the last
-// non-empty bin). nb is 2048 or 1024.
+// Key histogram scan from the highest bin down: the bin where the running total first reaches
+// `target` (before < target <= before + h). Returns 1 with bin/above when target <= total;
+// otherwise 0, or with `clamp` target = total (the last non-empty bin). nb is 2048 or 1024.
+template <typename T>
+__device__ inline T hist_at(SelShared& s, uint32_t i);
+template <>
+__device__ inline double hist_at<double>(SelShared& s, uint32_t i) { return (double)s.hd[i] / kFx; }
+template <>
+__device__ inline uint32_t hist_at<uint32_t>(SelShared& s, uint32_t i) { return s.hu[i]; }
+
 template <typename T>
 __device__ inline int hist_cross(SelShared& s, uint32_t nb, T target, uint32_t* bin, T* above,
                                  bool clamp = false) {
     const uint32_t tid = threadIdx.x;
-    const uint32_t per = nb / kSelThreads;  // 1 or 2
-    T* h = (T*)(sizeof(T) == 8 ? (void*)s.hd : (void*)s.hu);
+    const uint32_t per = nb / kSelThreads;
     T loc = T(0);
-    for (uint32_t j = 0; j < per; ++j) loc += h[nb - 1u - (tid * per + j)];
+    for (uint32_t j = 0; j < per; ++j) loc += hist_at<T>(s, nb - 1u - (tid * per + j));
     T tot;
     T before = block_excl_scan(loc, s, &tot);
     if (target > tot) {
@@ -140,7 +159,7 @@ __device__ inline int hist_cross(SelShared& s, uint32_t nb, T target, uint32_t* 
     __syncthreads();
     for (uint32_t j = 0; j < per; ++j) {
         const uint32_t bi = nb - 1u - (tid * per + j);
-        const T hv = h[bi];
+        const T hv = hist_at<T>(s, bi);
         if (before < target && target <= before + hv) {
             s.bu[0] = bi;
             if (sizeof(T) == 8) s.bd[0] = (double)before;
@@ -160,23 +179,99 @@ __device__ inline int hist_cross(SelShared& s, uint32_t nb, T target, uint32_t* 
     return 1;
 }
 
+// Bitonic sort of s.cand[0, n) ascending (pads to the next power of two with ~0).
+__device__ inline void sort_cand(SelShared& s, uint32_t n) {
+    const uint32_t tid = threadIdx.x;
+    uint32_t P = 2;
+    while (P < n) P <<= 1;
+    for (uint32_t i = n + tid; i < P; i += kSelThreads) s.cand[i] = ~0ull;
+    __syncthreads();
+    for (uint32_t size = 2; size <= P; size <<= 1) {
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            for (uint32_t i = tid; i < P / 2; i += kSelThreads) {
+                const uint32_t lo = 2 * i - (i & (stride - 1));
+                const uint32_t hi = lo + stride;
+                const bool up = ((lo & size) == 0);
+                const unsigned long long x = s.cand[lo], y = s.cand[hi];
+                if ((x > y) == up) { s.cand[lo] = y; s.cand[hi] = x; }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// Visits every (value, index) of a row with kInflight independent loads per thread in flight.
+template <class F>
+__device__ inline void row_pass(const float* l, uint32_t V, F&& f) {
+    const uint32_t tid = threadIdx.x;
+    if ((V & 3u) == 0u && ((uintptr_t)l & 15u) == 0u) {
+        const float4* l4 = reinterpret_cast<const float4*>(l);
+        const uint32_t V4 = V >> 2;
+        for (uint32_t base = 0; base < V4; base += kInflight * kSelThreads) {
+            float4 q[kInflight];
+#pragma unroll
+            for (int j = 0; j < kInflight; ++j) {
+                const uint32_t idx = base + (uint32_t)j * kSelThreads + tid;
+                q[j] = (idx < V4) ? l4[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int j = 0; j < kInflight; ++j) {
+                const uint32_t idx = base + (uint32_t)j * kSelThreads + tid;
+                if (idx < V4) {
+                    f(q[j].x, 4u * idx);
+                    f(q[j].y, 4u * idx + 1u);
+                    f(q[j].z, 4u * idx + 2u);
+                    f(q[j].w, 4u * idx + 3u);
+                }
+            }
+        }
+    } else {
+        for (uint32_t base = 0; base < V; base += 4u * kInflight * kSelThreads) {
+            float q[4 * kInflight];
+#pragma unroll
+            for (int j = 0; j < 4 * kInflight; ++j) {
+                const uint32_t idx = base + (uint32_t)j * kSelThreads + tid;
+                q[j] = (idx < V) ? l[idx] : 0.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < 4 * kInflight; ++j) {
+                const uint32_t idx = base + (uint32_t)j * kSelThreads + tid;
+                if (idx < V) f(q[j], idx);
+            }
+        }
+    }
+}
+
 // ---- per-row context ---------------------------------------------------------------------------
 
 struct RowCtx {
-    uint32_t b, V;
+    uint32_t V;
     const float* l;      // row logits
     float m;             // row max
     float T;             // temperature
-    uint2* list;         // compaction scratch [V]
+    uint2* list;         // compaction scratch [V] (radix fallback)
+    float inv_w;         // value bins: bin(l) = (m - l) * inv_w, clamped to the last bin
 };
 
-// Weight of logit v in mode 0 (count), 1 (exp(v - m)), 2 (exp((v - m) / T)).
-__device__ inline double weight(const RowCtx& c, float v, int mode) {
-    if (mode == 0) return 1.0;
-    if (v == -INFINITY) return 0.0;
-    const double d = (double)v - (double)c.m;
-    if (mode == 1) return (double)expf((float)d);
-    return (double)expf((float)(d / (double)c.T));
+// Equal-width value bins over [lo, m], bin 0 holding the largest logits. Monotone in the logit,
+// so bin order is rank order. -inf and values below lo land in the last bin.
+__device__ inline uint32_t vbin(const RowCtx& c, float l) {
+    const float d = (c.m - l) * c.inv_w;
+    return (d < (float)(kVBins - 1)) ? (uint32_t)d : kVBins - 1u;
+}
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ inline unsigned long long to_fx(float w) {
+    return (unsigned long long)(w * 1099511627776.0f);
+}
+
+// Weight of logit v: mode 0 count, 1 exp(v - m), 2 exp((v - m) / T); hardware exp2.
+__device__ inline float weight_f(const RowCtx& c, float v, int mode) {
+    if (mode == 0) return 1.0f;
+    if (v == -INFINITY) return 0.0f;
+    const float k = (mode == 1) ? kLog2e : kLog2e / c.T;
+    return __builtin_amdgcn_exp2f((v - c.m) * k);
 }
 
 // Prefix set in (key desc, id asc) order: bounded by element (kb, ib) inclusive, or everything.
@@ -188,15 +283,16 @@ struct PSet {
     }
 };
 
+// ---- radix fallback ------------------------------------------------------------------------------
+
 // Radix select over ids: the j-th smallest id (0-based) among list entries with key == kx.
 __device__ inline uint32_t select_tied_id(SelShared& s, const uint2* list, uint32_t n, uint32_t kx,
                                           uint32_t j) {
     const uint32_t tid = threadIdx.x;
     uint32_t prefix = 0, mask = 0, rem = j + 1;  // rank from the bottom, 1-based
-    const int shifts[3] = {21, 10, 0};
-    const uint32_t nbs[3] = {2048u, 2048u, 1024u};
     for (int lv = 0; lv < 3; ++lv) {
-        const uint32_t nb = nbs[lv], sh = (uint32_t)shifts[lv];
+        const uint32_t nb = (lv < 2) ? 2048u : 1024u;
+        const uint32_t sh = (lv == 0) ? 21u : (lv == 1) ? 10u : 0u;
         for (uint32_t i = tid; i < kBins; i += kSelThreads) s.hu[i] = 0u;
         __syncthreads();
         for (uint32_t i = tid; i < n; i += kSelThreads) {
@@ -204,8 +300,7 @@ __device__ inline uint32_t select_tied_id(SelShared& s, const uint2* list, uint3
             if (e.x == kx && (e.y & mask) == prefix) atomicAdd(&s.hu[(e.y >> sh) & (nb - 1u)], 1u);
         }
         __syncthreads();
-        // ascending scan: smallest ids first. Reverse the bin order for hist_cross (which scans
-        // from the top) by reading bins mirrored.
+        // smallest ids first: mirror the bins for hist_cross, which scans from the top
         for (uint32_t i = tid; i < nb / 2; i += kSelThreads) {
             const uint32_t t = s.hu[i];
             s.hu[i] = s.hu[nb - 1u - i];
@@ -227,53 +322,46 @@ __device__ inline uint32_t select_tied_id(SelShared& s, const uint2* list, uint3
 __device__ int find_cross(SelShared& s, const RowCtx& c, const PSet& ps, int mode, double target,
                           uint32_t* kx, uint32_t* ix) {
     const uint32_t tid = threadIdx.x;
-    // level 1: 11-bit histogram over the row
-    for (uint32_t i = tid; i < kBins; i += kSelThreads) s.hd[i] = 0.0;
+    for (uint32_t i = tid; i < kBins; i += kSelThreads) s.hd[i] = 0ull;
     __syncthreads();
-    for (uint32_t i = tid; i < c.V; i += kSelThreads) {
-        const float v = c.l[i];
+    row_pass(c.l, c.V, [&](float v, uint32_t i) {
         const uint32_t k = float_key(v);
-        if (!ps.has(k, i)) continue;
-        const double w = weight(c, v, mode);
-        if (w != 0.0) atomicAdd(&s.hd[k >> 21], w);
-    }
+        if (!ps.has(k, i)) return;
+        const float w = weight_f(c, v, mode);
+        if (w != 0.0f) atomicAdd(&s.hd[k >> 21], to_fx(w));
+    });
     __syncthreads();
     uint32_t d1;
     double above;
     if (!hist_cross<double>(s, kBins, target, &d1, &above)) return 0;
     double rem = target - above;
-    // compact bucket d1 (set members) into the list
     if (tid == 0) s.bu[2] = 0u;
     __syncthreads();
-    for (uint32_t i = tid; i < c.V; i += kSelThreads) {
-        const float v = c.l[i];
+    row_pass(c.l, c.V, [&](float v, uint32_t i) {
         const uint32_t k = float_key(v);
-        if ((k >> 21) != d1 || !ps.has(k, i)) continue;
+        if ((k >> 21) != d1 || !ps.has(k, i)) return;
         const uint32_t slot = atomicAdd(&s.bu[2], 1u);
         c.list[slot] = make_uint2(k, i);
-    }
+    });
     __syncthreads();
     const uint32_t n = s.bu[2];
     __syncthreads();
-    // levels 2 and 3 on the list
     uint32_t prefix = d1 << 21, mask = 0xFFE00000u;
-    const int shifts[2] = {10, 0};
-    const uint32_t nbs[2] = {2048u, 1024u};
     for (int lv = 0; lv < 2; ++lv) {
-        const uint32_t nb = nbs[lv], sh = (uint32_t)shifts[lv];
-        for (uint32_t i = tid; i < kBins; i += kSelThreads) s.hd[i] = 0.0;
+        const uint32_t nb = (lv == 0) ? 2048u : 1024u;
+        const uint32_t sh = (lv == 0) ? 10u : 0u;
+        for (uint32_t i = tid; i < kBins; i += kSelThreads) s.hd[i] = 0ull;
         __syncthreads();
         for (uint32_t i = tid; i < n; i += kSelThreads) {
             const uint2 e = c.list[i];
             if ((e.x & mask) != prefix) continue;
-            const double w = weight(c, key_float(e.x), mode);
-            if (w != 0.0) atomicAdd(&s.hd[(e.x >> sh) & (nb - 1u)], w);
+            const float w = weight_f(c, key_float(e.x), mode);
+            if (w != 0.0f) atomicAdd(&s.hd[(e.x >> sh) & (nb - 1u)], to_fx(w));
         }
         __syncthreads();
         uint32_t d;
         double ab;
-        // The bucket's weight was summed in another order at the previous level, so a target
-        // within rounding of the bucket total may exceed this level's total: clamp it.
+        // the bucket's weight was summed in another order at the previous level: clamp
         if (!hist_cross<double>(s, nb, rem, &d, &ab, true)) return 0;
         rem -= ab;
         prefix |= d << sh;
@@ -281,13 +369,13 @@ __device__ int find_cross(SelShared& s, const RowCtx& c, const PSet& ps, int mod
     }
     const uint32_t kk = prefix;
     // ties: equal keys have equal weight w; the crossing is the j-th smallest tied id with
-    // (j + 1) * w >= rem.
+    // (j + 1) * w >= rem
     uint32_t nt = 0;
     for (uint32_t i = tid; i < n; i += kSelThreads) nt += (c.list[i].x == kk) ? 1u : 0u;
     nt = block_sum<uint32_t>(nt, s);
-    const double w = weight(c, key_float(kk), mode);
+    const double w = (double)weight_f(c, key_float(kk), mode);
     uint32_t j = 0;
-    if (w > 0.0) {
+    if (w > 0.0 && nt > 0u) {
         const double q = ceil(rem / w) - 1.0;
         j = (q <= 0.0) ? 0u : (q >= (double)(nt - 1u) ? nt - 1u : (uint32_t)q);
     }
@@ -295,6 +383,179 @@ __device__ int find_cross(SelShared& s, const RowCtx& c, const PSet& ps, int mod
     if (id == 0xFFFFFFFFu) return 0;
     *kx = kk;
     *ix = id;
+    return 1;
+}
+
+// ---- full-vocabulary path on value bins ------------------------------------------------------------
+
+// Bins [0, limit) of h scanned from bin 0: the bin where the running weight first reaches
+// target. Returns 1 with bin/above; 0 with *above = the total of the range otherwise.
+__device__ inline int scan_cross(SelShared& s, const unsigned long long* h, uint32_t limit, double target,
+                                 uint32_t* bin, double* above) {
+    const uint32_t tid = threadIdx.x;
+    const uint32_t per = kVBins / kSelThreads;
+    double loc = 0.0;
+    for (uint32_t j = 0; j < per; ++j) {
+        const uint32_t bi = tid * per + j;
+        if (bi < limit) loc += (double)h[bi] / kFx;
+    }
+    double tot;
+    double before = block_excl_scan<double>(loc, s, &tot);
+    if (tid == 0) s.bu[0] = 0xFFFFFFFFu;
+    __syncthreads();
+    for (uint32_t j = 0; j < per; ++j) {
+        const uint32_t bi = tid * per + j;
+        const double hv = (bi < limit) ? (double)h[bi] / kFx : 0.0;
+        if (hv > 0.0 && before < target && target <= before + hv) {
+            s.bu[0] = bi;
+            s.bd[0] = before;
+        }
+        before += hv;
+    }
+    __syncthreads();
+    const uint32_t r = s.bu[0];
+    const double ab = s.bd[0];
+    __syncthreads();
+    if (r == 0xFFFFFFFFu) {
+        *above = tot;
+        return 0;
+    }
+    *bin = r;
+    *above = ab;
+    return 1;
+}
+
+// Within the sorted list s.cand, elements [lo, hi] (inclusive, at most kCandCap): the first
+// index whose cumulative weight (exp2((v - m) * kw)) reaches rem, or hi; *sum receives the
+// weight of [lo, hi]. Thread t owns elements lo + [kPer t, kPer t + kPer).
+constexpr uint32_t kPer = kCandCap / kSelThreads;
+
+__device__ uint32_t list_cross(SelShared& s, const RowCtx& c, uint32_t lo, uint32_t hi, float kw,
+                               double rem, double* sum) {
+    const uint32_t tid = threadIdx.x;
+    double wv[kPer];
+    double lsum = 0.0;
+#pragma unroll
+    for (uint32_t t = 0; t < kPer; ++t) {
+        const uint32_t e = lo + kPer * tid + t;
+        double w = 0.0;
+        if (e <= hi) {
+            const float v = key_float(~(uint32_t)(s.cand[e] >> 32));
+            if (v != -INFINITY) w = (double)__builtin_amdgcn_exp2f((v - c.m) * kw);
+        }
+        wv[t] = w;
+        lsum += w;
+    }
+    double tot;
+    double run = block_excl_scan<double>(lsum, s, &tot);
+    if (sum) *sum = tot;
+    uint32_t first = 0xFFFFFFFFu;
+#pragma unroll
+    for (uint32_t t = 0; t < kPer; ++t) {
+        run += wv[t];
+        const uint32_t e = lo + kPer * tid + t;
+        if (e <= hi && first == 0xFFFFFFFFu && run >= rem) first = e;
+    }
+    first = block_min_u(first, s);
+    return first == 0xFFFFFFFFu ? hi : first;
+}
+
+// Index of the first sorted list element (of n) whose value bin is >= bin.
+__device__ uint32_t list_bin_start(SelShared& s, const RowCtx& c, uint32_t n, uint32_t bin) {
+    uint32_t first = 0xFFFFFFFFu;
+    for (uint32_t e = threadIdx.x; e < n; e += kSelThreads)
+        if (vbin(c, key_float(~(uint32_t)(s.cand[e] >> 32))) >= bin) first = min(first, e);
+    first = block_min_u(first, s);
+    return first == 0xFFFFFFFFu ? n : first;
+}
+
+// Nucleus over the full distribution, then the temperature draw over the survivors. Returns 1
+// with *token, 0 when a bin is too large to gather (the caller uses the radix fallback).
+__device__ int full_vocab_value_path(SelShared& s, const RowCtx& c, float top_p, float u,
+                                     uint32_t first_id, uint32_t* token, double* denom_out,
+                                     double* r_out) {
+    const uint32_t tid = threadIdx.x;
+    const float kq = kLog2e / c.T;
+    const bool same = (kq == kLog2e);  // T = 1: one weighting serves nucleus and draw
+    for (uint32_t i = tid; i < kVBins; i += kSelThreads) { s.vm[i] = 0ull; s.vq[i] = 0ull; }
+    __syncthreads();
+    row_pass(c.l, c.V, [&](float v, uint32_t) {
+        if (v == -INFINITY) return;
+        const uint32_t b = vbin(c, v);
+        const float d = v - c.m;
+        atomicAdd(&s.vm[b], to_fx(__builtin_amdgcn_exp2f(d * kLog2e)));
+        if (!same) atomicAdd(&s.vq[b], to_fx(__builtin_amdgcn_exp2f(d * kq)));
+    });
+    __syncthreads();
+    const unsigned long long* hq = same ? s.vm : s.vq;
+    uint32_t bb;
+    // nucleus bin: where the T = 1 weight reaches top_p of the row total
+    uint32_t cb = kVBins;
+    double target_w = 0.0, wabove = 0.0;
+    if (top_p < 1.0f) {
+        double total;
+        (void)scan_cross(s, s.vm, kVBins, INFINITY, &bb, &total);
+        target_w = (double)top_p * total;
+        if (!scan_cross(s, s.vm, kVBins, target_w, &cb, &wabove)) cb = kVBins;
+    }
+    // survivor weight bounds: A = bins above the nucleus bin, plus up to all of that bin
+    double A;
+    (void)scan_cross(s, hq, cb, INFINITY, &bb, &A);
+    const double Bq = (cb < kVBins) ? (double)hq[cb] / kFx : 0.0;
+    if (!(u > 0.0f)) {  // u = 0: the first element in sorted order
+        *token = first_id;
+        *denom_out = A;
+        *r_out = 0.0;
+        return 1;
+    }
+    const uint32_t lim = (cb < kVBins) ? cb + 1u : kVBins;
+    uint32_t dlo = cb, dhi = cb;
+    double ab;
+    if (!scan_cross(s, hq, lim, (double)u * A, &dlo, &ab)) dlo = lim - 1u;
+    if (!scan_cross(s, hq, lim, (double)u * (A + Bq), &dhi, &ab)) dhi = lim - 1u;
+    // gather {cb} and [dlo, dhi]
+    if (tid == 0) s.bu[2] = 0u;
+    __syncthreads();
+    row_pass(c.l, c.V, [&](float v, uint32_t i) {
+        const uint32_t b = vbin(c, v);
+        if (b != cb && (b < dlo || b > dhi)) return;
+        const uint32_t slot = atomicAdd(&s.bu[2], 1u);
+        if (slot < kCandCap) s.cand[slot] = ((unsigned long long)(~float_key(v)) << 32) | i;
+    });
+    __syncthreads();
+    const uint32_t n = s.bu[2];
+    __syncthreads();
+    if (n > kCandCap || n == 0u) return 0;
+    sort_cand(s, n);
+    // nucleus cut inside bin cb (its elements are the list's last block)
+    double denom = A;
+    uint32_t cstart = n, ecut = n - 1u;
+    if (cb < kVBins) {
+        cstart = list_bin_start(s, c, n, cb);
+        if (cstart >= n) return 0;
+        ecut = list_cross(s, c, cstart, n - 1u, kLog2e, target_w - wabove, nullptr);
+        double qin;
+        (void)list_cross(s, c, cstart, ecut, kq, INFINITY, &qin);
+        denom = A + qin;
+    }
+    const double r = (double)u * denom;
+    *denom_out = denom;
+    *r_out = r;
+    uint32_t e;
+    if (cb < kVBins && r > A) {
+        e = list_cross(s, c, cstart, ecut, kq, r - A, nullptr);
+    } else {
+        uint32_t db;
+        double dab;
+        if (!scan_cross(s, hq, cb, r, &db, &dab)) return 0;
+        if (db < dlo || db > dhi) return 0;  // outside the gathered range (rounding)
+        const uint32_t dstart = list_bin_start(s, c, n, db);
+        const uint32_t dend = list_bin_start(s, c, n, db + 1u);
+        if (dstart >= dend) return 0;
+        e = list_cross(s, c, dstart, dend - 1u, kq, r - dab, nullptr);
+    }
+    *token = (uint32_t)s.cand[e];
+    __syncthreads();
     return 1;
 }
 
@@ -307,23 +568,39 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a, uint2* __r
     const DevRow row = a.rows[b];
     const float u = a.uniforms ? a.uniforms[b] : row.u;
     const BlockPartial* parts = a.partials + (size_t)b * a.ntile;
+    const bool keys_cached = a.ntile <= kKeyCache;
 
-    // 1. row max, lowest argmax, total mass from the block partials.
-    float bm = -INFINITY;
+    // 1. row max, lowest argmax and finite minimum over the block partials; the block-maximum
+    //    keys are kept in LDS for the shortlist threshold
+    float bm = -INFINITY, bmin = INFINITY;
     uint32_t ba = 0xFFFFFFFFu;
-    for (uint32_t t = tid; t < a.ntile; t += kSelThreads) {
-        const BlockPartial p = parts[t];
-        if (p.max > bm || (p.max == bm && p.arg < ba)) { bm = p.max; ba = p.arg; }
+    for (uint32_t t0 = tid; t0 < a.ntile; t0 += 4u * kSelThreads) {
+        BlockPartial p[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t t = t0 + (uint32_t)j * kSelThreads;
+            if (t < a.ntile) p[j] = parts[t];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t t = t0 + (uint32_t)j * kSelThreads;
+            if (t >= a.ntile) continue;
+            if (p[j].max > bm || (p[j].max == bm && p[j].arg < ba)) { bm = p[j].max; ba = p[j].arg; }
+            bmin = fminf(bmin, p[j].minf);
+            if (keys_cached) s.pkey[t] = float_key(p[j].max);
+        }
     }
     wave_argmax(bm, ba);
-    if (lane == 0) { s.wmax[wave] = bm; s.warg[wave] = ba; }
+    bmin = wave_min(bmin);
+    if (lane == 0) { s.wmax[wave] = bm; s.warg[wave] = ba; s.wmin[wave] = bmin; }
     __syncthreads();
-    float m = s.wmax[0];
+    float m = s.wmax[0], fmin = s.wmin[0];
     uint32_t arg = s.warg[0];
     for (uint32_t w = 1; w < kSelWaves; ++w) {
         const float v = s.wmax[w];
         const uint32_t i = s.warg[w];
         if (v > m || (v == m && i < arg)) { m = v; arg = i; }
+        fmin = fminf(fmin, s.wmin[w]);
     }
     __syncthreads();
 
@@ -337,11 +614,12 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a, uint2* __r
         rep.shortlist = 1;
         rep.cut = 1;
     } else {
+        // 2. Z = sum_t exp(max_t - m) * sumexp_t (fp32 exp, double sum)
         double zl = 0.0;
         if (m != -INFINITY)
             for (uint32_t t = tid; t < a.ntile; t += kSelThreads) {
                 const BlockPartial p = parts[t];
-                if (p.max != -INFINITY) zl += exp((double)p.max - (double)m) * (double)p.sumexp;
+                if (p.max != -INFINITY) zl += (double)(__builtin_amdgcn_exp2f((p.max - m) * kLog2e) * p.sumexp);
             }
         const double Z = block_sum<double>(zl, s);
         rep.total = Z;
@@ -349,39 +627,38 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a, uint2* __r
         const uint32_t want = row.want;
         rep.shortlist = want;
         bool general = (want > kMaxTopK);
+        auto pkey = [&](uint32_t t) { return keys_cached ? s.pkey[t] : float_key(parts[t].max); };
         if (!(Z > 0.0) || m == -INFINITY) {
             token = 0xFFFFFFFFu;
             rep.path = 3;
             general = false;
         } else if (!general) {
             // ---- shortlist path ----
+            // tau: lower edge of the 22-bit key bin holding the want-th largest block maximum
             uint32_t tau = 0u;
             if (a.ntile > want) {
                 uint32_t prefix = 0, mask = 0, rem = want;
-                const int shifts[3] = {21, 10, 0};
-                const uint32_t nbs[3] = {2048u, 2048u, 1024u};
-                for (int lv = 0; lv < 3; ++lv) {
-                    const uint32_t nb = nbs[lv], sh = (uint32_t)shifts[lv];
+                for (int lv = 0; lv < 2; ++lv) {
+                    const uint32_t sh = (lv == 0) ? 21u : 10u;
                     for (uint32_t i = tid; i < kBins; i += kSelThreads) s.hu[i] = 0u;
                     __syncthreads();
                     for (uint32_t t = tid; t < a.ntile; t += kSelThreads) {
-                        const uint32_t k = float_key(parts[t].max);
-                        if ((k & mask) == prefix) atomicAdd(&s.hu[(k >> sh) & (nb - 1u)], 1u);
+                        const uint32_t k = pkey(t);
+                        if ((k & mask) == prefix) atomicAdd(&s.hu[(k >> sh) & (kBins - 1u)], 1u);
                     }
                     __syncthreads();
                     uint32_t bin = 0, above = 0;
-                    hist_cross<uint32_t>(s, nb, rem, &bin, &above);
+                    hist_cross<uint32_t>(s, kBins, rem, &bin, &above);
                     rem -= above;
                     prefix |= bin << sh;
-                    mask |= (nb - 1u) << sh;
+                    mask |= (kBins - 1u) << sh;
                 }
                 tau = prefix;
             }
-            // qualifying blocks
             if (tid == 0) { s.bu[3] = 0u; s.bu[4] = 0u; }
             __syncthreads();
             for (uint32_t t = tid; t < a.ntile; t += kSelThreads) {
-                if (float_key(parts[t].max) >= tau) {
+                if (pkey(t) >= tau) {
                     const uint32_t slot = atomicAdd(&s.bu[3], 1u);
                     if (slot < kTileCap) s.tiles[slot] = t;
                 }
@@ -391,14 +668,24 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a, uint2* __r
             if (nq > kTileCap) {
                 general = true;
             } else {
-                for (uint32_t j = wave; j < nq; j += kSelWaves) {
-                    const uint32_t id = s.tiles[j] * kTileRows + lane;
-                    if (id < a.V) {
-                        const uint32_t k = float_key(lrow[id]);
+                // gather elements >= tau from the qualifying blocks, 8 loads in flight per thread
+                const uint32_t items = nq * kTileRows;
+                for (uint32_t it0 = tid; it0 < items; it0 += 8u * kSelThreads) {
+                    float v[8];
+                    uint32_t id[8];
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        const uint32_t it = it0 + (uint32_t)t * kSelThreads;
+                        id[t] = (it < items) ? s.tiles[it >> 6] * kTileRows + (it & 63u) : 0xFFFFFFFFu;
+                        v[t] = (id[t] < a.V) ? lrow[id[t]] : -INFINITY;
+                    }
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        if (id[t] >= a.V) continue;
+                        const uint32_t k = float_key(v[t]);
                         if (k >= tau) {
                             const uint32_t slot = atomicAdd(&s.bu[4], 1u);
-                            if (slot < kCandCap)
-                                s.cand[slot] = ((unsigned long long)(~k) << 32) | id;
+                            if (slot < kCandCap) s.cand[slot] = ((unsigned long long)(~k) << 32) | id[t];
                         }
                     }
                 }
@@ -407,22 +694,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a, uint2* __r
                 if (n > kCandCap) general = true;
                 __syncthreads();
                 if (!general) {
-                    uint32_t P = 2;
-                    while (P < n) P <<= 1;
-                    for (uint32_t i = n + tid; i < P; i += kSelThreads) s.cand[i] = ~0ull;
-                    __syncthreads();
-                    for (uint32_t size = 2; size <= P; size <<= 1) {
-                        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-                            for (uint32_t i = tid; i < P / 2; i += kSelThreads) {
-                                const uint32_t lo = 2 * i - (i & (stride - 1));
-                                const uint32_t hi = lo + stride;
-                                const bool up = ((lo & size) == 0);
-                                const unsigned long long x = s.cand[lo], y = s.cand[hi];
-                                if ((x > y) == up) { s.cand[lo] = y; s.cand[hi] = x; }
-                            }
-                            __syncthreads();
-                        }
-                    }
+                    sort_cand(s, n);
                     const uint32_t W = min(want, n);
                     float li = -INFINITY;
                     uint32_t idi = 0;
@@ -460,71 +732,48 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a, uint2* __r
             }
         }
         if (general) {
-            // ---- general path: weighted radix select over the whole row ----
             RowCtx c;
-            c.b = b;
             c.V = a.V;
             c.l = lrow;
             c.m = m;
             c.T = row.temperature;
             c.list = scratch + (size_t)b * a.V;
-            PSet s0 = {0, 0u, 0u};
-            if (want < a.V) {
-                uint32_t kx, ix;
-                if (find_cross(s, c, s0, 0, (double)want, &kx, &ix)) s0 = PSet{1, kx, ix};
-            }
-            PSet s1 = s0;
-            if (row.top_p < 1.0f) {
-                uint32_t kx, ix;
-                if (find_cross(s, c, s0, 1, (double)row.top_p * Z, &kx, &ix)) s1 = PSet{1, kx, ix};
-            }
-            // survivor weight, survivor count, and the last survivor (smallest element)
-            double dl = 0.0;
-            uint32_t cl = 0;
-            uint32_t lk = 0xFFFFFFFFu, li = 0u;  // smallest key, then largest id
-            for (uint32_t i = tid; i < a.V; i += kSelThreads) {
-                const float v = lrow[i];
-                const uint32_t k = float_key(v);
-                if (!s1.has(k, i)) continue;
-                dl += weight(c, v, 2);
-                ++cl;
-                if (k < lk || (k == lk && i > li)) { lk = k; li = i; }
-            }
-            const double denom = block_sum<double>(dl, s);
-            const uint32_t cut = block_sum<uint32_t>(cl, s);
-            // smallest key then largest id: reduce (lk, ~li) with min
-            const unsigned long long lkey = ((unsigned long long)lk << 32) | (uint32_t)(~li);
-            {
-                unsigned long long v = lkey;
-#pragma unroll
-                for (int o = 32; o > 0; o >>= 1) {
-                    const unsigned long long ov = __shfl_xor(v, o, 64);
-                    v = ov < v ? ov : v;
+            const float span = 48.0f * fmaxf(1.0f, row.temperature);
+            const float lo = fmaxf(fmin, m - span);
+            c.inv_w = (m > lo) ? (float)kVBins / (m - lo) : 0.0f;
+            bool done = false;
+            if (want >= a.V) {
+                double dn = 0.0, rr = 0.0;
+                uint32_t tk = 0;
+                if (full_vocab_value_path(s, c, row.top_p, u, arg, &tk, &dn, &rr)) {
+                    token = tk;
+                    rep.denom = dn;
+                    rep.r = rr;
+                    rep.path = 2;
+                    done = true;
                 }
-                __syncthreads();
-                if (lane == 0) s.cand[wave] = v;
-                __syncthreads();
-                if (tid == 0) {
-                    unsigned long long best = s.cand[0];
-                    for (uint32_t w = 1; w < kSelWaves; ++w) best = s.cand[w] < best ? s.cand[w] : best;
-                    s.bu[6] = ~(uint32_t)best;
-                }
-                __syncthreads();
             }
-            const uint32_t last_id = s1.bounded ? s1.ib : s.bu[6];
-            const double r = (double)u * denom;
-            uint32_t kx, ix;
-            if (r <= 0.0) {
-                token = arg;  // first element in sorted order
-            } else if (find_cross(s, c, s1, 2, r, &kx, &ix)) {
-                token = ix;
-            } else {
-                token = last_id;
+            if (!done) {
+                // radix fallback: shortlist bound, nucleus, then the draw
+                uint32_t kx, ix;
+                PSet s0 = {0, 0u, 0u};
+                if (want < a.V && find_cross(s, c, s0, 0, (double)want, &kx, &ix)) s0 = PSet{1, kx, ix};
+                PSet s1 = s0;
+                if (row.top_p < 1.0f && find_cross(s, c, s0, 1, (double)row.top_p * Z, &kx, &ix))
+                    s1 = PSet{1, kx, ix};
+                double dl = 0.0;
+                row_pass(lrow, a.V, [&](float v, uint32_t i) {
+                    if (s1.has(float_key(v), i)) dl += (double)weight_f(c, v, 2);
+                });
+                const double tot = block_sum<double>(dl, s);
+                const double r = (double)u * tot;
+                if (!(r > 0.0)) token = arg;
+                else if (find_cross(s, c, s1, 2, r, &kx, &ix)) token = ix;
+                else token = s1.bounded ? s1.ib : arg;
+                rep.denom = tot;
+                rep.r = r;
+                rep.path = 4;
             }
-            rep.cut = cut;
-            rep.denom = denom;
-            rep.r = r;
-            rep.path = 2;
         }
     }
 
