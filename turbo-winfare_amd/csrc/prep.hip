@@ -1,9 +1,12 @@
-// Create-time repack and per-step preparation kernels.
+// Create-time repack and the per-step preparation kernel.
 //
 //  k_repack_w / k_repack_sb : reference layout -> tiled layout (once, at create)
-//  k_prep                   : final RMSNorm (src/cpu_reference.cpp:43-52) and the activation
-//                             formats the head kernels read
-//  k_modtable               : per-row sorted modifier list (history counts + summed bias)
+//  k_step_prep              : blocks [0, B): final RMSNorm (src/cpu_reference.cpp:43-52) and
+//                             the activation format the head kernel reads (digit planes for
+//                             B <= 2, k-permuted fp16 for B > 2); block 0 also copies the staged
+//                             per-row parameters to device memory. Blocks [B, 2B), when a row
+//                             has history or bias entries: the row's modifier table sorted by id
+//                             (history counts + summed bias) and its first entry per 64-id block.
 #include <algorithm>
 #include <stdexcept>
 #include <string>
