@@ -25,6 +25,9 @@ FLAGS = [
     "-std=c++20",
     "-fPIC",
     "-fvisibility=hidden",
+    # Fused multiply-add stays on by default, but `#pragma clang fp contract(off)` is honoured
+    # where results must round like the reference's separate operations.
+    "-ffp-contract=fast-honor-pragmas",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{PKG.parent / 'include'}",
 ]

@@ -38,7 +38,6 @@ void set_error(const std::string& m) { g_last_error = m; }
 void clear_error() { g_last_error.clear(); }
 
 constexpr int kMaxBatch = 256;
-constexpr uint32_t kModCap = 8192;  // history + bias entries per row (64 KiB of LDS sort keys)
 
 struct HandleBox {
     uint32_t magic = 0x54445448u;  // "TDTH"
@@ -427,7 +426,7 @@ TURBO_DT_API void* turbo_lmhead_create(const TurboLMHeadDesc* d) {
         h.eps = d->rms_norm_eps;
         h.stream = nullptr;
         h.max_batch = kMaxBatch;
-        h.mod_cap = kModCap;
+        h.mod_cap = tdt::kModCap;
 
         const size_t wbytes = static_cast<size_t>(h.V) * (h.D / 2u);
         const size_t gcount = static_cast<size_t>(h.V) * h.G;

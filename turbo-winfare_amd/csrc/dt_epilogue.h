@@ -6,6 +6,9 @@
 //   presence / frequency                                 (extension)
 //   ban          -> -inf                                 (extension)
 // then stores the logit (optional) and the block partial (max, lowest argmax, sum exp(l-max)).
+// Floating-point contraction is off in these functions (the library is built with
+// -ffp-contract=fast-honor-pragmas): a fused multiply-add would round once where the reference
+// rounds twice, e.g. in l - frequency * count or in cap * tanh(z / cap) + bias.
 #pragma once
 
 #include "dt_internal.h"
@@ -13,18 +16,19 @@
 namespace tdt {
 
 __device__ inline float apply_entry(float l, const ModEntry& m, const DevRow& row, float limit) {
-    if (m.has_bias) l = __fadd_rn(l, m.bias);
+#pragma clang fp contract(off)
+    if (m.has_bias) l = l + m.bias;
     if (m.count) {
         const float p = row.repetition_penalty;
         if (p != 1.0f) {
             for (uint32_t c = 0; c < m.count; ++c) {
-                l = (l > 0.0f) ? __fdiv_rn(l, p) : __fmul_rn(l, p);
+                l = (l > 0.0f) ? l / p : l * p;
                 if (limit > 0.0f) l = fminf(fmaxf(l, -limit), limit);
             }
         }
         if (row.presence_penalty != 0.0f || row.frequency_penalty != 0.0f) {
-            l = __fsub_rn(l, row.presence_penalty);
-            l = __fsub_rn(l, __fmul_rn(row.frequency_penalty, (float)m.count));
+            l = l - row.presence_penalty;
+            l = l - row.frequency_penalty * (float)m.count;
         }
     }
     return l;
@@ -33,10 +37,11 @@ __device__ inline float apply_entry(float l, const ModEntry& m, const DevRow& ro
 // acc: the raw head value of id = tile*64 + lane for batch row b (wave-uniform b and tile).
 __device__ inline void epilogue_wave(float acc, uint32_t b, uint32_t tile, uint32_t lane,
                                      const EpiArgs& ep) {
+#pragma clang fp contract(off)
     const uint32_t id = tile * kTileRows + lane;
     const bool valid = id < ep.V;
     float l = acc;
-    if (ep.cap > 0.0f) l = __fmul_rn(ep.cap, tanhf(__fdiv_rn(l, ep.cap)));
+    if (ep.cap > 0.0f) l = ep.cap * tanhf(l / ep.cap);
     const DevRow& row = ep.rows[b];
     if (row.has_mods && ep.block_start) {
         const uint32_t* bs = ep.block_start + (size_t)b * (ep.ntile + 1) + tile;

@@ -10,6 +10,12 @@
 namespace tdt {
 
 // Device-resident head plus per-step scratch. All sizes are fixed at create time.
+// History + bias entries one row's modifier table can hold (the sort runs in LDS).
+constexpr uint32_t kModCap = 8192;
+// Static LDS of the step-prep kernel, in u64 words: kModCap sort keys plus kModCap + 1 run
+// starts (u32); the RMSNorm blocks reuse it for the hidden row (D floats).
+constexpr uint32_t kPrepPoolU64 = kModCap + (kModCap + 2u) / 2u;
+
 struct Head {
     int device = 0;
     uint32_t V = 0;        // vocabulary rows

@@ -8,9 +8,10 @@
 namespace tdt {
 
 __global__ __launch_bounds__(256) void k_softcap(float* __restrict__ z, size_t n, float cap) {
+#pragma clang fp contract(off)
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    z[i] = __fmul_rn(cap, tanhf(__fdiv_rn(z[i], cap)));
+    z[i] = cap * tanhf(z[i] / cap);
 }
 
 void launch_softcap(float* z, size_t n, float cap, hipStream_t st) {
@@ -31,6 +32,7 @@ __global__ __launch_bounds__(kRepThreads) void k_repetition(float* __restrict__ 
                                                             const uint32_t* __restrict__ history,
                                                             uint32_t n, uint32_t P, float penalty,
                                                             float limit) {
+#pragma clang fp contract(off)
     extern __shared__ uint32_t ids[];  // [P]
     const uint32_t tid = threadIdx.x;
     for (uint32_t i = tid; i < P; i += kRepThreads) ids[i] = (i < n) ? history[i] : 0xFFFFFFFFu;
@@ -54,7 +56,7 @@ __global__ __launch_bounds__(kRepThreads) void k_repetition(float* __restrict__ 
         for (uint32_t j = i; j < P && ids[j] == id; ++j) ++count;
         float v = logits[id];
         for (uint32_t c = 0; c < count; ++c) {
-            v = (v > 0.0f) ? __fdiv_rn(v, penalty) : __fmul_rn(v, penalty);
+            v = (v > 0.0f) ? v / penalty : v * penalty;
             if (limit > 0.0f) v = fminf(fmaxf(v, -limit), limit);
         }
         logits[id] = v;

@@ -12,6 +12,7 @@
 #include <string>
 
 #include "dt_internal.h"
+#include "dt_sort.h"
 
 namespace tdt {
 
@@ -79,12 +80,14 @@ void launch_repack(const Head& h, const uint8_t* W, const uint16_t* S, const uin
 // Modifier table: history ids (when the row uses them) and bias entries are sorted together by
 // (id, source, position) with a bitonic sort in LDS. Each run of equal ids becomes one entry:
 // the history count and the bias values summed in list order from 0.0f. Entries are written
-// sorted by id; block_start[t] = number of entries with id < 64 t is scattered by the run
-// starts (run e fills the tiles after the previous run's tile up to its own).
+// sorted by id; block_start[t] = number of entries with id < 64 t comes from a binary search
+// over the run ids.
 constexpr uint32_t kPrepThreads = 1024;
 constexpr uint32_t kPrepWaves = kPrepThreads / 64;
+static_assert(kPrepPoolU64 * 8u >= 8192u * 4u, "the pool must hold the largest hidden row");
 
 __device__ void prep_row(const PrepArgs& a, uint32_t b, float* sx) {
+#pragma clang fp contract(off)
     __shared__ double red[kPrepWaves];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t D = a.D;
@@ -107,11 +110,11 @@ __device__ void prep_row(const PrepArgs& a, uint32_t b, float* sx) {
         const float ms = (float)(tot / (double)D);
         // sqrtf and 1.0f / s, each correctly rounded: computed in double and rounded once to
         // float, which is exact for sqrt and division (53 >= 2 * 24 + 2 bits).
-        const float sq = (float)sqrt((double)__fadd_rn(ms, a.eps));
+        const float sq = (float)sqrt((double)(ms + a.eps));
         const float inv = (float)(1.0 / (double)sq);
         for (uint32_t i = tid; i < D; i += kPrepThreads) {
-            float v = __fmul_rn(sx[i], inv);
-            if (a.gamma) v = __fmul_rn(v, bf16_to_f32(a.gamma[i]));
+            float v = sx[i] * inv;
+            if (a.gamma) v = v * bf16_to_f32(a.gamma[i]);
             sx[i] = v;
         }
         __syncthreads();
@@ -170,12 +173,14 @@ __device__ void prep_row(const PrepArgs& a, uint32_t b, float* sx) {
 }
 
 __device__ void modtable_row(const PrepArgs& a, uint32_t b, unsigned long long* keys) {
-    __shared__ uint32_t s_nruns;
+#pragma clang fp contract(off)
     __shared__ uint32_t s_scan[kPrepWaves];
+    __shared__ uint32_t s_nruns;
     const uint32_t tid = threadIdx.x;
     const uint32_t use = a.rows_src[b].has_mods;
     if (use == 0u) return;
     const uint32_t P = a.P, V = a.V;
+    uint32_t* rs = reinterpret_cast<uint32_t*>(keys + P);  // run starts, [nruns + 1] <= P + 1
     const uint32_t nh = ((use & 1u) && a.history) ? min(a.hist_len[b], a.hist_stride) : 0u;
     const uint32_t nb = ((use & 2u) && a.bias_ids) ? min(a.bias_count[b], a.bias_stride) : 0u;
     const unsigned long long kPad = ~0ull;
@@ -192,26 +197,17 @@ __device__ void modtable_row(const PrepArgs& a, uint32_t b, unsigned long long* 
         keys[i] = k;
     }
     __syncthreads();
-    for (uint32_t size = 2; size <= P; size <<= 1) {  // bitonic sort, ascending
-        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-            for (uint32_t i = tid; i < P / 2; i += kPrepThreads) {
-                const uint32_t lo = 2 * i - (i & (stride - 1));
-                const uint32_t hi = lo + stride;
-                const bool up = ((lo & size) == 0);
-                const unsigned long long x = keys[lo], y = keys[hi];
-                if ((x > y) == up) { keys[lo] = y; keys[hi] = x; }
-            }
-            __syncthreads();
-        }
-    }
-    // run starts -> compacted entry index via a block scan over per-thread counts
-    const uint32_t per = (P + kPrepThreads - 1) / kPrepThreads;
+    block_sort_u64<kPrepThreads>(keys, P);
+    // Run starts (first key of each id; pads sort last) -> entry index by a block scan over
+    // per-thread counts of consecutive keys.
+    const uint32_t per = (P + kPrepThreads - 1u) / kPrepThreads;
     const uint32_t i0 = tid * per;
-    uint32_t cnt = 0;
-    for (uint32_t i = i0; i < i0 + per && i < P; ++i) {
+    auto starts_run = [&](uint32_t i) {
         const unsigned long long k = keys[i];
-        if (k != kPad && (i == 0 || (keys[i - 1] >> 32) != (k >> 32))) ++cnt;
-    }
+        return k != kPad && (i == 0u || (keys[i - 1u] >> 32) != (k >> 32));
+    };
+    uint32_t cnt = 0;
+    for (uint32_t i = i0; i < i0 + per && i < P; ++i) cnt += starts_run(i) ? 1u : 0u;
     const uint32_t lane = tid & 63u, wave = tid >> 6;
     uint32_t incl = cnt;
 #pragma unroll
@@ -219,49 +215,52 @@ __device__ void modtable_row(const PrepArgs& a, uint32_t b, unsigned long long* 
         const uint32_t v = (uint32_t)__shfl_up((int)incl, o, 64);
         if ((int)lane >= o) incl += v;
     }
-    if (lane == 63) s_scan[wave] = incl;
+    if (lane == 63u) s_scan[wave] = incl;
     __syncthreads();
-    if (tid == 0) {
+    if (tid == 0u) {
         uint32_t run = 0;
         for (uint32_t w = 0; w < kPrepWaves; ++w) { const uint32_t t = s_scan[w]; s_scan[w] = run; run += t; }
         s_nruns = run;
     }
     __syncthreads();
     const uint32_t nruns = s_nruns;
-    const uint32_t ntile = a.ntile;
-    uint32_t* bs = a.block_start + (size_t)b * (ntile + 1);
     uint32_t e = s_scan[wave] + incl - cnt;
     for (uint32_t i = i0; i < i0 + per && i < P; ++i) {
-        const unsigned long long k = keys[i];
-        if (k == kPad || (i != 0 && (keys[i - 1] >> 32) == (k >> 32))) continue;
-        const uint32_t id = (uint32_t)(k >> 32);
-        uint32_t count = 0, has_bias = 0;
-        float total = 0.0f;
-        for (uint32_t j = i; j < P && keys[j] != kPad && (uint32_t)(keys[j] >> 32) == id; ++j) {
-            const uint32_t lo = (uint32_t)keys[j];
-            if (lo & 0x80000000u) {
-                total = __fadd_rn(total, a.bias_vals[(size_t)b * a.bias_stride + (lo & 0x7FFFFFFFu)]);
-                has_bias = 1;
-            } else {
-                ++count;
-            }
-        }
-        a.mods[(size_t)b * a.mod_cap + e] = ModEntry{id, count, total, has_bias};
-        // tiles (prev_tile, tile] start at entry e
-        const uint32_t tile = id / kTileRows;
-        const uint32_t first = (i == 0) ? 0u : (uint32_t)(keys[i - 1] >> 32) / kTileRows + 1u;
-        for (uint32_t t = first; t <= tile; ++t) bs[t] = e;
-        if (e + 1u == nruns)
-            for (uint32_t t = tile + 1u; t <= ntile; ++t) bs[t] = nruns;
-        ++e;
+        if (starts_run(i)) rs[e++] = i;
+        // the last valid key closes the final run
+        if (keys[i] != kPad && (i + 1u == P || keys[i + 1u] == kPad)) rs[nruns] = i + 1u;
     }
-    if (tid == 0) a.mod_count[b] = nruns;
-    if (nruns == 0u)
-        for (uint32_t t = tid; t <= ntile; t += kPrepThreads) bs[t] = 0u;
+    __syncthreads();
+    // One entry per run: history occurrences sort before the run's bias entries, which sort in
+    // list order and are summed in that order from 0.0f.
+    ModEntry* mods = a.mods + (size_t)b * a.mod_cap;
+    for (uint32_t r = tid; r < nruns; r += kPrepThreads) {
+        const uint32_t s0 = rs[r], s1 = rs[r + 1u];
+        uint32_t j = s1;
+        while (j > s0 && ((uint32_t)keys[j - 1u] & 0x80000000u)) --j;
+        float total = 0.0f;
+        for (uint32_t t = j; t < s1; ++t)
+            total = total + (a.bias_vals[(size_t)b * a.bias_stride + ((uint32_t)keys[t] & 0x7FFFFFFFu)]);
+        mods[r] = ModEntry{(uint32_t)(keys[s0] >> 32), j - s0, total, s1 > j ? 1u : 0u};
+    }
+    // block_start[t] = number of entries with id < 64 t: a binary search over the run ids.
+    const uint32_t ntile = a.ntile;
+    uint32_t* bs = a.block_start + (size_t)b * (ntile + 1u);
+    for (uint32_t t = tid; t <= ntile; t += kPrepThreads) {
+        const uint32_t target = t * kTileRows;
+        uint32_t lo = 0, hi = nruns;
+        while (lo < hi) {
+            const uint32_t mid = (lo + hi) >> 1;
+            if ((uint32_t)(keys[rs[mid]] >> 32) < target) lo = mid + 1u;
+            else hi = mid;
+        }
+        bs[t] = lo;
+    }
+    if (tid == 0u) a.mod_count[b] = nruns;
 }
 
 __global__ __launch_bounds__(kPrepThreads) void k_step_prep(PrepArgs a) {
-    extern __shared__ unsigned long long dyn[];
+    __shared__ unsigned long long pool[kPrepPoolU64];
     const uint32_t blk = blockIdx.x;
     if (blk == 0 && a.rows_dst) {
         const uint32_t* src = reinterpret_cast<const uint32_t*>(a.rows_src);
@@ -269,17 +268,16 @@ __global__ __launch_bounds__(kPrepThreads) void k_step_prep(PrepArgs a) {
         for (uint32_t i = threadIdx.x; i < (uint32_t)a.B * (sizeof(DevRow) / 4); i += kPrepThreads) dst[i] = src[i];
     }
     if (blk < (uint32_t)a.B) {
-        if (a.hidden) prep_row(a, blk, reinterpret_cast<float*>(dyn));
+        if (a.hidden) prep_row(a, blk, reinterpret_cast<float*>(pool));
     } else {
-        modtable_row(a, blk - (uint32_t)a.B, dyn);
+        modtable_row(a, blk - (uint32_t)a.B, pool);
     }
 }
 
 void launch_step_prep(const Head& h, const PrepArgs& a, bool with_mods, hipStream_t st) {
-    size_t lds = a.hidden ? (size_t)h.D * sizeof(float) : 0;
-    if (with_mods) lds = std::max(lds, (size_t)a.P * sizeof(unsigned long long));
+    // The pool holds D floats (checked at create) and kModCap keys + run starts (P <= mod_cap).
     const unsigned grid = (unsigned)a.B * (with_mods ? 2u : 1u);
-    hipLaunchKernelGGL(k_step_prep, dim3(grid), dim3(kPrepThreads), lds, st, a);
+    hipLaunchKernelGGL(k_step_prep, dim3(grid), dim3(kPrepThreads), 0, st, a);
     check_hip(hipGetLastError(), "step prep");
 }
 

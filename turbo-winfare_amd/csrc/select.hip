@@ -27,6 +27,7 @@
 #include <stdexcept>
 
 #include "dt_internal.h"
+#include "dt_sort.h"
 
 namespace tdt {
 
@@ -179,25 +180,13 @@ __device__ inline int hist_cross(SelShared& s, uint32_t nb, T target, uint32_t* 
     return 1;
 }
 
-// Bitonic sort of s.cand[0, n) ascending (pads to the next power of two with ~0).
+// Sorts s.cand[0, n) ascending (pads to the next power of two with ~0).
 __device__ inline void sort_cand(SelShared& s, uint32_t n) {
-    const uint32_t tid = threadIdx.x;
     uint32_t P = 2;
     while (P < n) P <<= 1;
-    for (uint32_t i = n + tid; i < P; i += kSelThreads) s.cand[i] = ~0ull;
+    for (uint32_t i = n + threadIdx.x; i < P; i += kSelThreads) s.cand[i] = ~0ull;
     __syncthreads();
-    for (uint32_t size = 2; size <= P; size <<= 1) {
-        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-            for (uint32_t i = tid; i < P / 2; i += kSelThreads) {
-                const uint32_t lo = 2 * i - (i & (stride - 1));
-                const uint32_t hi = lo + stride;
-                const bool up = ((lo & size) == 0);
-                const unsigned long long x = s.cand[lo], y = s.cand[hi];
-                if ((x > y) == up) { s.cand[lo] = y; s.cand[hi] = x; }
-            }
-            __syncthreads();
-        }
-    }
+    block_sort_u64<kSelThreads>(s.cand, P);
 }
 
 // Visits every (value, index) of a row with kInflight independent loads per thread in flight.
