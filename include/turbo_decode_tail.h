@@ -78,7 +78,8 @@ TURBO_DT_API void turbo_lmhead_destroy(void* handle);
 /* hip_stream is a hipStream_t (NULL = the null stream). Must be created at default priority. */
 TURBO_DT_API int turbo_lmhead_set_stream(void* handle, void* hip_stream);
 TURBO_DT_API int turbo_lmhead_synchronize(void* handle);
-/* Largest batch one step accepts, and the per-row modifier capacity (history + bias entries). */
+/* Largest batch one step accepts, and the largest bias_stride (logit-bias entries per row).
+ * History length is not limited. */
 TURBO_DT_API int turbo_lmhead_limits(void* handle, int* max_batch, int* max_row_modifiers);
 
 /* ---- sampling parameters ----------------------------------------------------------------- */

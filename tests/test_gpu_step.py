@@ -240,39 +240,43 @@ def test_sampler_paths(head, kind):
             assert paths[i] == 1, (i, paths[i])
 
 
-def test_modifier_table_at_capacity(head):
-    """History + bias lists up to the per-row capacity (8192 sorted entries): Zipf histories with
-    long runs of one id, ids out of range, duplicate bias ids summed in list order. The modified
-    logits must equal the oracle's modifiers bit-for-bit and the tokens the oracle sampler's."""
+def test_modifier_tables_at_capacity(head):
+    """Bias lists at the per-row capacity (bias_stride = limit, sorted in LDS) and histories far
+    longer than it (counted densely): Zipf histories with long runs of one id, ids out of range,
+    duplicate bias ids summed in list order. The modified logits must equal the oracle's
+    modifiers bit-for-bit and the tokens the oracle sampler's. A second call with other
+    histories checks that the first call's counts were cleared."""
     h, _ = head
     _, cap = h.limits()
-    nh, nb = cap - 1200, 1000
+    nh, nb = 12000, cap
     rows = [T.row_default(temperature=0.9, top_k=50, top_p=0.95, repetition_penalty=1.2,
                           presence_penalty=0.4, frequency_penalty=0.2, seed=31 + b, counter=2)
             for b in range(4)]
-    hists = np.stack([synth.zipf_ids(nh, V, 1.05, SEED + 70 + b) for b in range(4)]).astype(np.uint32)
-    hists[1, ::97] = V + 5                        # ignored (id >= vocab)
-    hl_np = np.array([nh, 3000, 0, 17], np.int32)
+    base = (synth.normal(SEED, 81, 4 * V).reshape(4, V) * 3).astype(np.float32)
     bl = [synth.bias_list(nb, V, -3.0, 3.0, SEED + 3, b) for b in range(4)]
     bids = np.stack([a for a, _ in bl]).astype(np.uint32)
     bids[:, 1::2] = bids[:, 0::2]                 # every id twice: summed in list order
-    bids[0, :50] = hists[0, 0]                    # bias on the most repeated history id
     bvals = np.stack([v for _, v in bl])
-    bc_np = np.array([nb, 0, 600, nb], np.int32)
-    base = (synth.normal(SEED, 81, 4 * V).reshape(4, V) * 3).astype(np.float32)
-    toks, after, _ = sample_given(h, base, rows, history=dev(hists.view(np.int32)),
-                                  history_len=dev(hl_np), bias_ids=dev(bids.view(np.int32)),
-                                  bias_values=dev(bvals), bias_count=dev(bc_np))
-    for b in range(4):
-        want = O.apply_modifiers(base[b], oparams(rows[b]), 30.0, history=hists[b, :hl_np[b]],
-                                 bias_ids=bids[b, :bc_np[b]], bias_values=bvals[b, :bc_np[b]])
-        bad = np.nonzero(after[b].view(np.uint32) != want.view(np.uint32))[0]
-        hc = np.bincount(hists[b, :hl_np[b]][hists[b, :hl_np[b]] < V], minlength=V)
-        bcnt = np.bincount(bids[b, :bc_np[b]], minlength=V)
-        detail = [(int(i), int(hc[i]), int(bcnt[i]), float(base[b, i]), float(after[b, i]), float(want[i]))
-                  for i in bad[:8]]
-        assert bad.size == 0, (b, int(bad.size), detail)
-    check_sampler_on_gpu_logits(rows, toks, after, [T.row_uniform(r) for r in rows])
+    bc_np = np.array([nb, 0, 600, 1000], np.int32)
+    for call in range(2):
+        hists = np.stack([synth.zipf_ids(nh, V, 1.05 + 0.1 * call, SEED + 70 + 4 * call + b)
+                          for b in range(4)]).astype(np.uint32)
+        hists[1, ::97] = V + 5                    # ignored (id >= vocab)
+        bids[0, :50] = hists[0, 0]                # bias on the most repeated history id
+        hl_np = np.array([nh, 3000, 0, 17], np.int32) if call == 0 else np.array([500, nh, 40, 0], np.int32)
+        toks, after, _ = sample_given(h, base, rows, history=dev(hists.view(np.int32)),
+                                      history_len=dev(hl_np), bias_ids=dev(bids.view(np.int32)),
+                                      bias_values=dev(bvals), bias_count=dev(bc_np))
+        for b in range(4):
+            want = O.apply_modifiers(base[b], oparams(rows[b]), 30.0, history=hists[b, :hl_np[b]],
+                                     bias_ids=bids[b, :bc_np[b]], bias_values=bvals[b, :bc_np[b]])
+            bad = np.nonzero(after[b].view(np.uint32) != want.view(np.uint32))[0]
+            hc = np.bincount(hists[b, :hl_np[b]][hists[b, :hl_np[b]] < V], minlength=V)
+            bcnt = np.bincount(bids[b, :bc_np[b]], minlength=V)
+            detail = [(int(i), int(hc[i]), int(bcnt[i]), float(base[b, i]), float(after[b, i]), float(want[i]))
+                      for i in bad[:8]]
+            assert bad.size == 0, (call, b, int(bad.size), detail)
+        check_sampler_on_gpu_logits(rows, toks, after, [T.row_uniform(r) for r in rows])
 
 
 def test_digit_path_modifiers_bit_exact(head):

@@ -14,7 +14,7 @@
 #include <stdexcept>
 #include <string>
 
-#include "../../include/turbo_decode_tail.h"
+#include "turbo_decode_tail.h"
 #include "dt_internal.h"
 
 namespace tdt {
@@ -152,6 +152,8 @@ void free_head(Head& h) {
     dfree(h.mods);
     dfree(h.mod_count);
     dfree(h.block_start);
+    dfree(h.hcount);
+    dfree(h.hbits);
     dfree(h.list_scratch);
     if (h.ring_host) (void)hipHostFree(h.ring_host);
     for (int i = 0; i < Head::kRing; ++i)
@@ -196,6 +198,9 @@ tdt::PrepArgs prep_args(const Head& h, const tdt::DevRow* src, int B) {
     a.P = 2;
     a.mods = h.mods;
     a.mod_cap = h.mod_cap;
+    a.hcount = h.hcount;
+    a.hbits = h.hbits;
+    a.hbw = h.hbw;
     a.mod_count = h.mod_count;
     a.block_start = h.block_start;
     return a;
@@ -250,6 +255,9 @@ tdt::EpiArgs epi_args(const Head& h, float* logits, bool softcap) {
     ep.mods = h.mods;
     ep.mod_cap = h.mod_cap;
     ep.block_start = h.block_start;
+    ep.hcount = h.hcount;
+    ep.hbits = h.hbits;
+    ep.hbw = h.hbw;
     ep.ban = nullptr;
     ep.ban_stride = 0;
     ep.rep_limit = (h.cap > 0.0f) ? h.cap * 0.9999f : 0.0f;
@@ -269,13 +277,11 @@ void launch_head(HandleBox& bx, int B, const tdt::EpiArgs& ep) {
         bx.t_accum_n += h.t_count;
         h.t_count = 0;
     }
-    if (timed) check_hip(hipEventRecord(h.t_start[h.t_count], h.stream), "timer start");
-    if (B <= 2) tdt::launch_head_digits(h, B, ep, h.stream);
-    else tdt::launch_head_mfma(h, B, ep, h.stream);
-    if (timed) {
-        check_hip(hipEventRecord(h.t_stop[h.t_count], h.stream), "timer stop");
-        ++h.t_count;
-    }
+    hipEvent_t ev0 = timed ? h.t_start[h.t_count] : nullptr;
+    hipEvent_t ev1 = timed ? h.t_stop[h.t_count] : nullptr;
+    if (B <= 2) tdt::launch_head_digits(h, B, ep, h.stream, ev0, ev1);
+    else tdt::launch_head_mfma(h, B, ep, h.stream, ev0, ev1);
+    if (timed) ++h.t_count;
 }
 
 tdt::HeadPath path_for(int B) { return B <= 2 ? tdt::HeadPath::Digits : tdt::HeadPath::Mfma; }
@@ -317,8 +323,7 @@ int run_rows(HandleBox& bx, const TurboStepInputs* in, const TurboStepOutputs* o
         rows[b] = make_devrow(h, r, mods);
     }
     uint32_t P = 2;
-    if (any_mods)
-        P = tdt::modtable_sort_size(h, (has_hist ? in->history_stride : 0u) + (has_bias ? in->bias_stride : 0u));
+    if (has_bias) P = tdt::modtable_sort_size(h, in->bias_stride);
     float* logits = given_logits ? given_logits : (out->logits ? out->logits : (all_greedy ? nullptr : h.logits));
 
     int pos = 0;
@@ -329,6 +334,7 @@ int run_rows(HandleBox& bx, const TurboStepInputs* in, const TurboStepOutputs* o
     pa.normed = (in->flags & TURBO_STEP_NORMED) ? 1 : 0;
     pa.path = path_for(B) == tdt::HeadPath::Digits ? 0 : 1;
     pa.P = P;
+    for (int b = 0; b < B; ++b) pa.mod_bits[b >> 4] |= (rows[b].has_mods & 3u) << (2 * (b & 15));
     if (has_hist) {
         pa.history = in->history;
         pa.hist_stride = in->history_stride;
@@ -362,6 +368,14 @@ int run_rows(HandleBox& bx, const TurboStepInputs* in, const TurboStepOutputs* o
         sa.hist_stride = in->history_stride;
         sa.hist_len = in->history_len;
     }
+    if (has_hist) {
+        sa.clr_history = in->history;
+        sa.clr_stride = in->history_stride;
+        sa.clr_len = in->history_len;
+    }
+    sa.hcount = h.hcount;
+    sa.hbits = h.hbits;
+    sa.hbw = h.hbw;
     tdt::launch_select(h, B, sa, h.stream);
     return 1;
 }
@@ -474,6 +488,11 @@ TURBO_DT_API void* turbo_lmhead_create(const TurboLMHeadDesc* d) {
         h.mods = dalloc<tdt::ModEntry>(MB * h.mod_cap, "alloc mods");
         h.mod_count = dalloc<uint32_t>(MB, "alloc mod_count");
         h.block_start = dalloc<uint32_t>(MB * (h.ntile + 1u), "alloc block_start");
+        h.hbw = (h.V + 31u) / 32u;
+        h.hcount = dalloc<uint32_t>(MB * h.V, "alloc history counts");
+        h.hbits = dalloc<uint32_t>(MB * h.hbw, "alloc history bitmap");
+        check_hip(hipMemset(h.hcount, 0, MB * h.V * sizeof(uint32_t)), "clear history counts");
+        check_hip(hipMemset(h.hbits, 0, MB * h.hbw * sizeof(uint32_t)), "clear history bitmap");
         h.list_scratch = dalloc<uint2>(MB * h.V, "alloc list scratch");
         check_hip(hipHostMalloc(reinterpret_cast<void**>(&h.ring_host),
                                 sizeof(tdt::DevRow) * MB * Head::kRing,

@@ -40,7 +40,7 @@ struct DevRow {
     float u;            // uniform for the draw (ignored when injected uniforms are given)
     uint32_t flags;     // kFlagFullVocab
     uint32_t want;      // shortlist size: top_k, else 256, else vocab (full-vocab mode)
-    uint32_t has_mods;  // modifier table built for this row
+    uint32_t has_mods;  // bit 0: history counts (repetition / presence / frequency); bit 1: bias table
     uint32_t pad[2];
 };
 

@@ -22,8 +22,10 @@ __device__ inline float apply_entry(float l, const ModEntry& m, const DevRow& ro
         const float p = row.repetition_penalty;
         if (p != 1.0f) {
             for (uint32_t c = 0; c < m.count; ++c) {
-                l = (l > 0.0f) ? l / p : l * p;
-                if (limit > 0.0f) l = fminf(fmaxf(l, -limit), limit);
+                float v = (l > 0.0f) ? l / p : l * p;
+                if (limit > 0.0f) v = fminf(fmaxf(v, -limit), limit);
+                if (v == l) break;  // a fixed point (0, or the clamp): later occurrences keep it
+                l = v;
             }
         }
         if (row.presence_penalty != 0.0f || row.frequency_penalty != 0.0f) {
@@ -32,6 +34,27 @@ __device__ inline float apply_entry(float l, const ModEntry& m, const DevRow& ro
         }
     }
     return l;
+}
+
+// The modifiers of one id of batch row b: its history count (dense array, read only where the
+// id's bit is set) and its summed bias (the row's bias entries of tile `tile`).
+__device__ inline ModEntry lookup_mods(uint32_t id, uint32_t b, uint32_t tile, const DevRow& row,
+                                       const EpiArgs& ep) {
+    ModEntry m{id, 0u, 0.0f, 0u};
+    if ((row.has_mods & 1u) && ep.hcount) {
+        const uint32_t w = ep.hbits[(size_t)b * ep.hbw + (id >> 5)];
+        if ((w >> (id & 31u)) & 1u) m.count = ep.hcount[(size_t)b * ep.V + id];
+    }
+    if ((row.has_mods & 2u) && ep.block_start) {
+        const uint32_t* bs = ep.block_start + (size_t)b * (ep.ntile + 1) + tile;
+        const uint32_t s = bs[0], e = bs[1];
+        const ModEntry* me = ep.mods + (size_t)b * ep.mod_cap;
+        for (uint32_t k = s; k < e; ++k) {
+            const ModEntry t = me[k];
+            if (t.id == id) { m.bias = t.bias; m.has_bias = 1u; }
+        }
+    }
+    return m;
 }
 
 // acc: the raw head value of id = tile*64 + lane for batch row b (wave-uniform b and tile).
@@ -43,14 +66,9 @@ __device__ inline void epilogue_wave(float acc, uint32_t b, uint32_t tile, uint3
     float l = acc;
     if (ep.cap > 0.0f) l = ep.cap * tanhf(l / ep.cap);
     const DevRow& row = ep.rows[b];
-    if (row.has_mods && ep.block_start) {
-        const uint32_t* bs = ep.block_start + (size_t)b * (ep.ntile + 1) + tile;
-        const uint32_t s = bs[0], e = bs[1];
-        const ModEntry* me = ep.mods + (size_t)b * ep.mod_cap;
-        for (uint32_t k = s; k < e; ++k) {
-            const ModEntry m = me[k];
-            if (m.id == id) l = apply_entry(l, m, row, ep.rep_limit);
-        }
+    if (row.has_mods && valid) {
+        const ModEntry m = lookup_mods(id, b, tile, row, ep);
+        if (m.count || m.has_bias) l = apply_entry(l, m, row, ep.rep_limit);
     }
     if (ep.ban && valid) {
         const uint32_t w = ep.ban[(size_t)b * ep.ban_stride + (id >> 5)];

@@ -9,13 +9,14 @@
 
 namespace tdt {
 
-// Device-resident head plus per-step scratch. All sizes are fixed at create time.
-// History + bias entries one row's modifier table can hold (the sort runs in LDS).
+// Logit-bias entries one row's bias table can hold (the sort runs in LDS). History length is
+// not limited: occurrences are counted in a dense per-row array.
 constexpr uint32_t kModCap = 8192;
 // Static LDS of the step-prep kernel, in u64 words: kModCap sort keys plus kModCap + 1 run
 // starts (u32); the RMSNorm blocks reuse it for the hidden row (D floats).
 constexpr uint32_t kPrepPoolU64 = kModCap + (kModCap + 2u) / 2u;
 
+// Device-resident head plus per-step scratch. All sizes are fixed at create time.
 struct Head {
     int device = 0;
     uint32_t V = 0;        // vocabulary rows
@@ -34,7 +35,7 @@ struct Head {
     uint16_t* gamma = nullptr;   // [D] bf16 or null
 
     int max_batch = 0;
-    uint32_t mod_cap = 0;        // max modifier entries per row (history + bias)
+    uint32_t mod_cap = 0;        // max bias entries per row
 
     // Per-step scratch.
     float* xn = nullptr;         // [max_batch][D] normalised activations
@@ -45,7 +46,12 @@ struct Head {
     float* logits = nullptr;     // [max_batch][V] scratch logits
     BlockPartial* partials = nullptr;  // [max_batch][ntile]
     DevRow* rows = nullptr;      // [max_batch]
-    ModEntry* mods = nullptr;    // [max_batch][mod_cap]
+    ModEntry* mods = nullptr;    // [max_batch][mod_cap] bias table sorted by id
+    // History occurrence counts, zero between steps: the step prep adds, the head epilogue
+    // reads, the select kernel clears exactly the entries the step set.
+    uint32_t* hcount = nullptr;  // [max_batch][V]
+    uint32_t* hbits = nullptr;   // [max_batch][hbw] bit per id with a nonzero count
+    uint32_t hbw = 0;            // ceil(V / 32)
     uint32_t* mod_count = nullptr;     // [max_batch]
     uint32_t* block_start = nullptr;   // [max_batch][ntile + 1]
     void* list_scratch = nullptr;      // [max_batch][V] uint2 compaction lists (select)
@@ -73,9 +79,12 @@ struct EpiArgs {
     float* logits;             // [B][V] or null (not written)
     BlockPartial* partials;    // [B][ntile]
     const DevRow* rows;        // [B]
-    const ModEntry* mods;      // [B][mod_cap] or null
+    const ModEntry* mods;      // [B][mod_cap] bias tables (rows with has_mods & 2)
     uint32_t mod_cap;
-    const uint32_t* block_start;  // [B][ntile + 1] or null
+    const uint32_t* block_start;  // [B][ntile + 1] first bias entry per tile
+    const uint32_t* hcount;    // [B][V] history counts (rows with has_mods & 1)
+    const uint32_t* hbits;     // [B][hbw]
+    uint32_t hbw;
     const uint32_t* ban;       // [B][ban_stride] or null
     uint32_t ban_stride;
     float rep_limit;           // 0.9999 * softcap used by the repetition clamp (0 = none)
@@ -87,7 +96,7 @@ enum class HeadPath { Digits, Mfma };
 struct PrepArgs {
     int B;
     const DevRow* rows_src;      // host-mapped staging slot (or device memory)
-    DevRow* rows_dst;            // device row buffer, filled by block 0 (null: skip the copy)
+    DevRow* rows_dst;            // device row buffer, filled by block 0 (null: no copy block)
     // activations (null hidden: no activation work)
     const void* hidden;
     int dtype;                   // 0 fp32, 1 bf16
@@ -101,8 +110,11 @@ struct PrepArgs {
     float* xws;
     float* xsum;
     uint16_t* x16;
-    // modifier table
-    uint32_t V, ntile, P;
+    // history counts and the bias table
+    uint32_t V, ntile, P;        // P: bias sort size (power of two >= bias_stride)
+    uint32_t* hcount;
+    uint32_t* hbits;
+    uint32_t hbw;
     const uint32_t* history;
     uint32_t hist_stride;
     const uint32_t* hist_len;
@@ -114,6 +126,8 @@ struct PrepArgs {
     uint32_t mod_cap;
     uint32_t* mod_count;
     uint32_t* block_start;
+    uint32_t mod_bits[16];       // 2 bits per row (DevRow::has_mods), so no block reads the
+                                 // host-mapped staging slot except the row copy
 };
 void launch_repack(const Head& h, const uint8_t* W, const uint16_t* S, const uint16_t* B,
                    hipStream_t st);
@@ -121,8 +135,12 @@ void launch_step_prep(const Head& h, const PrepArgs& a, bool with_mods, hipStrea
 uint32_t modtable_sort_size(const Head& h, uint32_t n);
 
 // gemv_digits.hip / gemm_mfma.hip
-void launch_head_digits(const Head& h, int batch, const EpiArgs& ep, hipStream_t st);
-void launch_head_mfma(const Head& h, int batch, const EpiArgs& ep, hipStream_t st);
+// ev0 / ev1 (may be null): timing events stamped by the head kernel's own dispatch
+// (hipExtLaunchKernelGGL), so timing adds no packets between kernels.
+void launch_head_digits(const Head& h, int batch, const EpiArgs& ep, hipStream_t st,
+                        hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
+void launch_head_mfma(const Head& h, int batch, const EpiArgs& ep, hipStream_t st,
+                      hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
 // epilogue over caller logits (no GEMV): logits are read, modified and summarised in place.
 void launch_logits_epilogue(const Head& h, int batch, const EpiArgs& ep, hipStream_t st);
 
@@ -139,6 +157,13 @@ struct SelectArgs {
     uint32_t* history;            // append target or null
     uint32_t hist_stride;
     uint32_t* hist_len;
+    // history whose counts the step set (rows with has_mods & 1): cleared here
+    const uint32_t* clr_history;
+    uint32_t clr_stride;
+    const uint32_t* clr_len;
+    uint32_t* hcount;
+    uint32_t* hbits;
+    uint32_t hbw;
 };
 void launch_select(const Head& h, int batch, const SelectArgs& a, hipStream_t st);
 

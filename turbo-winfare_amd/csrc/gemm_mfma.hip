@@ -26,6 +26,8 @@
 //    computes, one barrier per group.
 //  * Epilogue in place on the accumulators: per (column, 64-row tile), lane-local reductions
 //    and one cross-lane exchange give the block partial; logits leave as float4 stores.
+#include <hip/hip_ext.h>
+
 #include <stdexcept>
 #include <utility>
 
@@ -209,20 +211,38 @@ __global__ __launch_bounds__(256 * NWN, OCC) void k_head_mfma(
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[mb][nb][r] = softcap_fast(acc[mb][nb][r], ep.cap);
         }
-        if (col_ok && ep.rows[bq].has_mods && ep.block_start) {
+        if (col_ok && ep.rows[bq].has_mods) {
             const DevRow row = ep.rows[bq];
-            const uint32_t* bs = ep.block_start + (size_t)bq * (ep.ntile + 1) + tile;
-            const uint32_t s = bs[0], e = bs[1];
+            // history counts: the two bitmap words of this tile decide which ids to look up
+            uint32_t hb[2] = {0u, 0u};
+            if ((row.has_mods & 1u) && ep.hcount) {
+                const uint32_t* hw = ep.hbits + (size_t)bq * ep.hbw + (base >> 5);
+                hb[0] = hw[0];
+                if (base + 32u < ep.V) hb[1] = hw[1];
+            }
+            uint32_t s = 0, e = 0;
             const ModEntry* me = ep.mods + (size_t)bq * ep.mod_cap;
-            for (uint32_t k = s; k < e; ++k) {
-                const ModEntry m = me[k];
-                const uint32_t ro = m.id - base;
+            if ((row.has_mods & 2u) && ep.block_start) {
+                const uint32_t* bs = ep.block_start + (size_t)bq * (ep.ntile + 1) + tile;
+                s = bs[0];
+                e = bs[1];
+            }
+            if ((hb[0] | hb[1]) != 0u || s < e) {
 #pragma unroll
                 for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        if (32u * mb + acc_row(r, hl) == ro)
+                    for (int r = 0; r < 16; ++r) {
+                        const uint32_t rr = 32u * mb + acc_row(r, hl);
+                        const uint32_t id = base + rr;
+                        ModEntry m{id, 0u, 0.0f, 0u};
+                        if ((hb[mb] >> (rr & 31u)) & 1u) m.count = ep.hcount[(size_t)bq * ep.V + id];
+                        for (uint32_t k = s; k < e; ++k) {
+                            const ModEntry t = me[k];
+                            if (t.id == id) { m.bias = t.bias; m.has_bias = 1u; }
+                        }
+                        if (m.count || m.has_bias)
                             acc[mb][nb][r] = apply_entry(acc[mb][nb][r], m, row, ep.rep_limit);
+                    }
             }
         }
         uint32_t ban0 = 0u, ban1 = 0u;
@@ -289,12 +309,13 @@ __global__ __launch_bounds__(256 * NWN, OCC) void k_head_mfma(
     }(std::make_integer_sequence<int, NB>{});
 }
 
-void launch_head_mfma(const Head& h, int batch, const EpiArgs& ep, hipStream_t st) {
+void launch_head_mfma(const Head& h, int batch, const EpiArgs& ep, hipStream_t st, hipEvent_t ev0,
+                      hipEvent_t ev1) {
     const unsigned grid = (h.ntile + 3u) / 4u;
     const uint32_t B = (uint32_t)batch;
 #define TDT_LAUNCH(NB, NWN, PF, OCC)                                                           \
-    hipLaunchKernelGGL((k_head_mfma<NB, NWN, PF, OCC>), dim3(grid), dim3(256 * NWN), 0, st, h.Wt, \
-                       h.SBt, h.x16, B, h.D, h.NC, h.G, ep)
+    hipExtLaunchKernelGGL((k_head_mfma<NB, NWN, PF, OCC>), dim3(grid), dim3(256 * NWN), 0, st, ev0, \
+                          ev1, 0, h.Wt, h.SBt, h.x16, B, h.D, h.NC, h.G, ep)
     if (B <= 32) TDT_LAUNCH(1, 1, 4, 4);
     else if (B <= 64) TDT_LAUNCH(2, 1, 4, 3);
     else if (B <= 128) TDT_LAUNCH(4, 1, 2, 1);

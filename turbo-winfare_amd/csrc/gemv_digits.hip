@@ -15,6 +15,8 @@
 //        row += s * (D_g * 2^(e-21)) + (8 s + b) * S_g,   D_g = sum q'_j X_j,  S_g = sum X_j 2^(e-21)
 //  * Per-group scale/bias come from the tiled (s | b << 16) words, one coalesced dword per lane.
 //  * Loads are software-pipelined kPF groups ahead.
+#include <hip/hip_ext.h>
+
 #include "dt_epilogue.h"
 
 namespace tdt {
@@ -97,14 +99,15 @@ __global__ __launch_bounds__(kDigitWaves * 64) void k_head_digits(
     for (int nb = 0; nb < NB; ++nb) epilogue_wave(acc[nb], (uint32_t)nb, tile, lane, ep);
 }
 
-void launch_head_digits(const Head& h, int batch, const EpiArgs& ep, hipStream_t st) {
+void launch_head_digits(const Head& h, int batch, const EpiArgs& ep, hipStream_t st,
+                        hipEvent_t ev0, hipEvent_t ev1) {
     const unsigned grid = (h.ntile + kDigitWaves - 1) / kDigitWaves;
     if (batch == 1)
-        hipLaunchKernelGGL(k_head_digits<1>, dim3(grid), dim3(kDigitWaves * 64), 0, st, h.Wt,
-                           h.SBt, h.xdig, h.xws, h.xsum, h.NC, h.G, ep);
+        hipExtLaunchKernelGGL(k_head_digits<1>, dim3(grid), dim3(kDigitWaves * 64), 0, st, ev0, ev1,
+                              0, h.Wt, h.SBt, h.xdig, h.xws, h.xsum, h.NC, h.G, ep);
     else if (batch == 2)
-        hipLaunchKernelGGL(k_head_digits<2>, dim3(grid), dim3(kDigitWaves * 64), 0, st, h.Wt,
-                           h.SBt, h.xdig, h.xws, h.xsum, h.NC, h.G, ep);
+        hipExtLaunchKernelGGL(k_head_digits<2>, dim3(grid), dim3(kDigitWaves * 64), 0, st, ev0, ev1,
+                              0, h.Wt, h.SBt, h.xdig, h.xws, h.xsum, h.NC, h.G, ep);
     else
         throw std::runtime_error("digit GEMV supports batch 1 or 2");
     check_hip(hipGetLastError(), "head (digit GEMV)");

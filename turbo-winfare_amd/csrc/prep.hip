@@ -1,12 +1,13 @@
 // Create-time repack and the per-step preparation kernel.
 //
 //  k_repack_w / k_repack_sb : reference layout -> tiled layout (once, at create)
-//  k_step_prep              : blocks [0, B): final RMSNorm (src/cpu_reference.cpp:43-52) and
-//                             the activation format the head kernel reads (digit planes for
-//                             B <= 2, k-permuted fp16 for B > 2); block 0 also copies the staged
-//                             per-row parameters to device memory. Blocks [B, 2B), when a row
-//                             has history or bias entries: the row's modifier table sorted by id
-//                             (history counts + summed bias) and its first entry per 64-id block.
+//  k_step_prep              : one block copies the staged per-row parameters to device memory;
+//                             one block per row runs the final RMSNorm
+//                             (src/cpu_reference.cpp:43-52) and writes the activation format the
+//                             head kernel reads (digit planes for B <= 2, k-permuted fp16 for
+//                             B > 2); one block per row with modifiers counts the row's history
+//                             occurrences per id and builds its bias table sorted by id (summed
+//                             bias) with its first entry per 64-id block.
 #include <algorithm>
 #include <stdexcept>
 #include <string>
@@ -61,10 +62,12 @@ void launch_repack(const Head& h, const uint8_t* W, const uint16_t* S, const uin
 }
 
 // ---- per-step preparation (one launch) -------------------------------------------------------
-// Blocks [0, B): one batch row each -- final RMSNorm (src/cpu_reference.cpp:43-52) and the
-//   activation format the head kernel reads. Block 0 also copies the per-row parameters from
-//   the host staging slot (pinned, mapped) into device memory for the later kernels.
-// Blocks [B, 2B) (only when some row uses modifiers): the row's modifier table.
+// Row copy block: the per-row parameters from the host staging slot (pinned, mapped) into
+//   device memory for the later kernels.
+// RMSNorm blocks, one per batch row: final RMSNorm (src/cpu_reference.cpp:43-52) and the
+//   activation format the head kernel reads.
+// Modifier blocks, one per batch row (only when some row uses modifiers): history counts and
+//   the bias table.
 //
 // Digit planes (small-batch GEMV): each 64-element group g is rescaled by 2^(21-e), where
 // max|x| = f * 2^e with f in [0.5, 1), and rounded to integers X with |X| <= 2^21. X is written
@@ -77,11 +80,13 @@ void launch_repack(const Head& h, const uint8_t* W, const uint16_t* S, const uin
 // (x0, x4, x1/16, x5/16, x2, x6, x3/16, x7/16): the order in which the weight dequant produces
 // halves, with odd elements divided by 16 because their weight halves carry a factor 16.
 //
-// Modifier table: history ids (when the row uses them) and bias entries are sorted together by
-// (id, source, position) with a bitonic sort in LDS. Each run of equal ids becomes one entry:
-// the history count and the bias values summed in list order from 0.0f. Entries are written
-// sorted by id; block_start[t] = number of entries with id < 64 t comes from a binary search
-// over the run ids.
+// History counts: every history occurrence with id < V adds one to hcount[b][id] and sets the
+// id's bit in hbits[b] (global atomics); the select kernel clears both after the head epilogue
+// has read them, so they are zero between steps.
+// Bias table: the bias entries are sorted by (id, list position) with a bitonic sort in LDS;
+// each run of equal ids becomes one entry whose value is the run's biases summed in list order
+// from 0.0f. Entries are written sorted by id; block_start[t] = number of entries with
+// id < 64 t comes from a binary search over the run ids.
 constexpr uint32_t kPrepThreads = 1024;
 constexpr uint32_t kPrepWaves = kPrepThreads / 64;
 static_assert(kPrepPoolU64 * 8u >= 8192u * 4u, "the pool must hold the largest hidden row");
@@ -177,22 +182,31 @@ __device__ void modtable_row(const PrepArgs& a, uint32_t b, unsigned long long* 
     __shared__ uint32_t s_scan[kPrepWaves];
     __shared__ uint32_t s_nruns;
     const uint32_t tid = threadIdx.x;
-    const uint32_t use = a.rows_src[b].has_mods;
-    if (use == 0u) return;
-    const uint32_t P = a.P, V = a.V;
+    const uint32_t use = (a.mod_bits[b >> 4] >> (2u * (b & 15u))) & 3u;
+    const uint32_t V = a.V;
+    if ((use & 1u) && a.history) {
+        // One count per occurrence (src/sampling.cpp:81-89 visits every occurrence); ids past
+        // the vocabulary are ignored (:82).
+        const uint32_t nh = min(a.hist_len[b], a.hist_stride);
+        const uint32_t* hist = a.history + (size_t)b * a.hist_stride;
+        for (uint32_t i = tid; i < nh; i += kPrepThreads) {
+            const uint32_t id = hist[i];
+            if (id < V) {
+                atomicAdd(a.hcount + (size_t)b * V + id, 1u);
+                atomicOr(a.hbits + (size_t)b * a.hbw + (id >> 5), 1u << (id & 31u));
+            }
+        }
+    }
+    if (!(use & 2u) || !a.bias_ids) return;
+    const uint32_t P = a.P;
     uint32_t* rs = reinterpret_cast<uint32_t*>(keys + P);  // run starts, [nruns + 1] <= P + 1
-    const uint32_t nh = ((use & 1u) && a.history) ? min(a.hist_len[b], a.hist_stride) : 0u;
-    const uint32_t nb = ((use & 2u) && a.bias_ids) ? min(a.bias_count[b], a.bias_stride) : 0u;
+    const uint32_t nb = min(a.bias_count[b], a.bias_stride);
     const unsigned long long kPad = ~0ull;
     for (uint32_t i = tid; i < P; i += kPrepThreads) {
         unsigned long long k = kPad;
-        if (i < nh) {
-            const uint32_t id = a.history[(size_t)b * a.hist_stride + i];
+        if (i < nb) {
+            const uint32_t id = a.bias_ids[(size_t)b * a.bias_stride + i];
             if (id < V) k = ((unsigned long long)id << 32) | i;
-        } else if (i < nh + nb) {
-            const uint32_t j = i - nh;
-            const uint32_t id = a.bias_ids[(size_t)b * a.bias_stride + j];
-            if (id < V) k = ((unsigned long long)id << 32) | 0x80000000ull | j;
         }
         keys[i] = k;
     }
@@ -231,17 +245,14 @@ __device__ void modtable_row(const PrepArgs& a, uint32_t b, unsigned long long* 
         if (keys[i] != kPad && (i + 1u == P || keys[i + 1u] == kPad)) rs[nruns] = i + 1u;
     }
     __syncthreads();
-    // One entry per run: history occurrences sort before the run's bias entries, which sort in
-    // list order and are summed in that order from 0.0f.
+    // One entry per id: its bias values summed in list order from 0.0f.
     ModEntry* mods = a.mods + (size_t)b * a.mod_cap;
     for (uint32_t r = tid; r < nruns; r += kPrepThreads) {
         const uint32_t s0 = rs[r], s1 = rs[r + 1u];
-        uint32_t j = s1;
-        while (j > s0 && ((uint32_t)keys[j - 1u] & 0x80000000u)) --j;
         float total = 0.0f;
-        for (uint32_t t = j; t < s1; ++t)
-            total = total + (a.bias_vals[(size_t)b * a.bias_stride + ((uint32_t)keys[t] & 0x7FFFFFFFu)]);
-        mods[r] = ModEntry{(uint32_t)(keys[s0] >> 32), j - s0, total, s1 > j ? 1u : 0u};
+        for (uint32_t t = s0; t < s1; ++t)
+            total = total + a.bias_vals[(size_t)b * a.bias_stride + (uint32_t)keys[t]];
+        mods[r] = ModEntry{(uint32_t)(keys[s0] >> 32), 0u, total, 1u};
     }
     // block_start[t] = number of entries with id < 64 t: a binary search over the run ids.
     const uint32_t ntile = a.ntile;
@@ -259,24 +270,36 @@ __device__ void modtable_row(const PrepArgs& a, uint32_t b, unsigned long long* 
     if (tid == 0u) a.mod_count[b] = nruns;
 }
 
+// Grid: [row copy block if rows_dst] [B RMSNorm blocks if hidden] [B table blocks if mods].
 __global__ __launch_bounds__(kPrepThreads) void k_step_prep(PrepArgs a) {
     __shared__ unsigned long long pool[kPrepPoolU64];
-    const uint32_t blk = blockIdx.x;
-    if (blk == 0 && a.rows_dst) {
-        const uint32_t* src = reinterpret_cast<const uint32_t*>(a.rows_src);
-        uint32_t* dst = reinterpret_cast<uint32_t*>(a.rows_dst);
-        for (uint32_t i = threadIdx.x; i < (uint32_t)a.B * (sizeof(DevRow) / 4); i += kPrepThreads) dst[i] = src[i];
+    uint32_t blk = blockIdx.x;
+    if (a.rows_dst) {
+        if (blk == 0u) {
+            // A PCIe round trip: on a block of its own, so no other block waits for it.
+            const uint32_t* src = reinterpret_cast<const uint32_t*>(a.rows_src);
+            uint32_t* dst = reinterpret_cast<uint32_t*>(a.rows_dst);
+            for (uint32_t i = threadIdx.x; i < (uint32_t)a.B * (sizeof(DevRow) / 4); i += kPrepThreads)
+                dst[i] = src[i];
+            return;
+        }
+        --blk;
     }
-    if (blk < (uint32_t)a.B) {
-        if (a.hidden) prep_row(a, blk, reinterpret_cast<float*>(pool));
-    } else {
-        modtable_row(a, blk - (uint32_t)a.B, pool);
+    if (a.hidden) {
+        if (blk < (uint32_t)a.B) {
+            prep_row(a, blk, reinterpret_cast<float*>(pool));
+            return;
+        }
+        blk -= (uint32_t)a.B;
     }
+    modtable_row(a, blk, pool);
 }
 
 void launch_step_prep(const Head& h, const PrepArgs& a, bool with_mods, hipStream_t st) {
     // The pool holds D floats (checked at create) and kModCap keys + run starts (P <= mod_cap).
-    const unsigned grid = (unsigned)a.B * (with_mods ? 2u : 1u);
+    const unsigned grid = (a.rows_dst ? 1u : 0u) + (a.hidden ? (unsigned)a.B : 0u) +
+                          (with_mods ? (unsigned)a.B : 0u);
+    if (grid == 0u) return;
     hipLaunchKernelGGL(k_step_prep, dim3(grid), dim3(kPrepThreads), 0, st, a);
     check_hip(hipGetLastError(), "step prep");
 }
@@ -285,7 +308,7 @@ uint32_t modtable_sort_size(const Head& h, uint32_t n) {
     uint32_t P = 2;
     while (P < n) P <<= 1;
     if (P > h.mod_cap)
-        throw std::runtime_error("history_stride + bias_stride exceeds the per-row modifier limit of " +
+        throw std::runtime_error("bias_stride exceeds the per-row bias-entry limit of " +
                                  std::to_string(h.mod_cap));
     return P;
 }

@@ -559,6 +559,20 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a, uint2* __r
     const BlockPartial* parts = a.partials + (size_t)b * a.ntile;
     const bool keys_cached = a.ntile <= kKeyCache;
 
+    // 0. the head epilogue has consumed this step's history counts: zero exactly the entries
+    //    the step prep set (ids of the first clr_len entries; the append below writes past them)
+    if ((row.has_mods & 1u) && a.clr_history && a.hcount) {
+        const uint32_t nh = min(a.clr_len[b], a.clr_stride);
+        const uint32_t* hist = a.clr_history + (size_t)b * a.clr_stride;
+        for (uint32_t i = tid; i < nh; i += kSelThreads) {
+            const uint32_t id = hist[i];
+            if (id < a.V) {
+                a.hcount[(size_t)b * a.V + id] = 0u;
+                a.hbits[(size_t)b * a.hbw + (id >> 5)] = 0u;
+            }
+        }
+    }
+
     // 1. row max, lowest argmax and finite minimum over the block partials; the block-maximum
     //    keys are kept in LDS for the shortlist threshold
     float bm = -INFINITY, bmin = INFINITY;
