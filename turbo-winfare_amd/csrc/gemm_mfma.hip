@@ -43,6 +43,15 @@ constexpr uint32_t kColHalves = 72;  // 64 halves of a group + 8 padding (LDS ba
 
 __device__ inline h2v as_h2(uint32_t u) { return __builtin_bit_cast(h2v, u); }
 
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+
+// The table is streamed once per step (nontemporal: it does not displace the activations).
+__device__ inline uint4 load_stream(const uint4* p) {
+    const v4u t = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+    return make_uint4(t.x, t.y, t.z, t.w);
+}
+__device__ inline uint32_t load_stream(const uint32_t* p) { return __builtin_nontemporal_load(p); }
+
 // 8 nibbles -> 8 halves (e0, e4, 16e1', 16e5', e2, e6, 16e3', 16e7') where e' = q s + b and the
 // primed slots carry the factor 16 (bias b16 = 16 b).
 __device__ inline h8v dequant_word(uint32_t w, h2v s2, h2v b2, h2v b16) {
@@ -137,8 +146,8 @@ __global__ __launch_bounds__(256 * NWN, OCC) void k_head_mfma(
         if ((uint32_t)p < G) {
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb) {
-                wr[p][mb] = *wptr(p, mb);
-                sbr[p][mb] = sbbase[(size_t)p * kTileRows + 32u * mb];
+                wr[p][mb] = load_stream(wptr(p, mb));
+                sbr[p][mb] = load_stream(sbbase + (size_t)p * kTileRows + 32u * mb);
             }
         }
     }
@@ -161,8 +170,8 @@ __global__ __launch_bounds__(256 * NWN, OCC) void k_head_mfma(
                 if (gn < G) {
 #pragma unroll
                     for (int mb = 0; mb < 2; ++mb) {
-                        wr[p][mb] = *wptr(gn, mb);
-                        sbr[p][mb] = sbbase[(size_t)gn * kTileRows + 32u * mb];
+                        wr[p][mb] = load_stream(wptr(gn, mb));
+                        sbr[p][mb] = load_stream(sbbase + (size_t)gn * kTileRows + 32u * mb);
                     }
                 }
                 const bool more = g + 1u < G;
