@@ -206,7 +206,7 @@ def sample_given(h, logits_np, rows, **kw):
     return tok.cpu().numpy().astype(np.uint32), lt.cpu().numpy(), rep.cpu().numpy()
 
 
-@pytest.mark.parametrize("kind", ["normal", "ties", "flat", "peaked", "banned"])
+@pytest.mark.parametrize("kind", ["normal", "ties", "flat", "peaked", "banned", "huge"])
 def test_sampler_paths(head, kind):
     h, _ = head
     Bn = 12
@@ -219,6 +219,9 @@ def test_sampler_paths(head, kind):
         base = (base * 6).astype(np.float32)
     elif kind == "banned":
         base[:, ::3] = -np.inf
+    elif kind == "huge":
+        # |max| > 1024: the shortlist bound takes the exact key-radix route
+        base = (base * 100 + 3000).astype(np.float32)
     cfgs = [(0.0, 1.0, 0, 0), (0.8, 0.95, 64, 0), (1.0, 0.9, 8, 0), (0.7, 1.0, 256, 0),
             (0.5, 1.0, 0, 0), (1.5, 0.99, 1, 0), (1.0, 0.9, 0, 1), (0.6, 0.5, 0, 1),
             (1.2, 1.0, 0, 1), (1.0, 0.99, 0, 1), (0.3, 0.8, 100, 1), (2.0, 0.7, 256, 0)]

@@ -63,7 +63,7 @@ struct SelShared {
             unsigned long long vq[kVBins];  // value-bin weights, temperature T, fixed point
         };
     };
-    unsigned long long cand[kCandCap];
+    __attribute__((aligned(16))) unsigned long long cand[kCandCap];
     uint32_t tiles[kTileCap];
     uint32_t pkey[kKeyCache];
     double wsum_d[kSelWaves];
@@ -71,6 +71,8 @@ struct SelShared {
     float wmax[kSelWaves];
     uint32_t warg[kSelWaves];
     float wmin[kSelWaves];
+    float wzm[kSelWaves];
+    double wzs[kSelWaves];
     double bd[4];
     uint32_t bu[8];
 };
@@ -180,11 +182,31 @@ __device__ inline int hist_cross(SelShared& s, uint32_t nb, T target, uint32_t* 
     return 1;
 }
 
-// Sorts s.cand[0, n) ascending (pads to the next power of two with ~0).
+// Sorts s.cand[0, n) ascending; keys are distinct (the low word is the id). Up to one key per
+// thread, each thread counts the keys below its own (wave-uniform LDS reads, which broadcast)
+// and stores its key at that rank; larger lists take the bitonic network.
 __device__ inline void sort_cand(SelShared& s, uint32_t n) {
+    const uint32_t tid = threadIdx.x;
+    if (n <= kSelThreads) {
+        unsigned long long k = 0;
+        uint32_t r = 0;
+        if (tid < n) {
+            k = s.cand[tid];
+            uint32_t j = 0;
+            for (; j + 2u <= n; j += 2u) {
+                const ulonglong2 pr = *reinterpret_cast<const ulonglong2*>(&s.cand[j]);
+                r += (pr.x < k ? 1u : 0u) + (pr.y < k ? 1u : 0u);
+            }
+            if (j < n) r += (s.cand[j] < k) ? 1u : 0u;
+        }
+        __syncthreads();
+        if (tid < n) s.cand[r] = k;
+        __syncthreads();
+        return;
+    }
     uint32_t P = 2;
     while (P < n) P <<= 1;
-    for (uint32_t i = n + threadIdx.x; i < P; i += kSelThreads) s.cand[i] = ~0ull;
+    for (uint32_t i = n + tid; i < P; i += kSelThreads) s.cand[i] = ~0ull;
     __syncthreads();
     block_sort_u64<kSelThreads>(s.cand, P);
 }
@@ -574,9 +596,12 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a, uint2* __r
     }
 
     // 1. row max, lowest argmax and finite minimum over the block partials; the block-maximum
-    //    keys are kept in LDS for the shortlist threshold
-    float bm = -INFINITY, bmin = INFINITY;
+    //    keys are kept in LDS for the shortlist threshold. Sampled rows also accumulate
+    //    Z = sum_t sumexp_t * exp(max_t - m) online (running maximum zm, rescaled sum zs).
+    const bool sampled = row.temperature > 0.0f;
+    float bm = -INFINITY, bmin = INFINITY, zm = -INFINITY;
     uint32_t ba = 0xFFFFFFFFu;
+    double zs = 0.0;
     for (uint32_t t0 = tid; t0 < a.ntile; t0 += 4u * kSelThreads) {
         BlockPartial p[4];
 #pragma unroll
@@ -591,11 +616,27 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a, uint2* __r
             if (p[j].max > bm || (p[j].max == bm && p[j].arg < ba)) { bm = p[j].max; ba = p[j].arg; }
             bmin = fminf(bmin, p[j].minf);
             if (keys_cached) s.pkey[t] = float_key(p[j].max);
+            if (sampled && p[j].max != -INFINITY) {
+                if (p[j].max > zm) {
+                    if (zm != -INFINITY) zs *= (double)__builtin_amdgcn_exp2f((zm - p[j].max) * kLog2e);
+                    zm = p[j].max;
+                }
+                zs += (double)(__builtin_amdgcn_exp2f((p[j].max - zm) * kLog2e) * p[j].sumexp);
+            }
         }
     }
     wave_argmax(bm, ba);
     bmin = wave_min(bmin);
-    if (lane == 0) { s.wmax[wave] = bm; s.warg[wave] = ba; s.wmin[wave] = bmin; }
+    if (sampled) {
+        const float wm = wave_max(zm);
+        zs = (zm == -INFINITY) ? 0.0 : zs * (double)__builtin_amdgcn_exp2f((zm - wm) * kLog2e);
+        zs = wave_sum_d(zs);
+        zm = wm;
+    }
+    if (lane == 0) {
+        s.wmax[wave] = bm; s.warg[wave] = ba; s.wmin[wave] = bmin;
+        s.wzm[wave] = zm; s.wzs[wave] = zs;
+    }
     __syncthreads();
     float m = s.wmax[0], fmin = s.wmin[0];
     uint32_t arg = s.warg[0];
@@ -605,6 +646,10 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a, uint2* __r
         if (v > m || (v == m && i < arg)) { m = v; arg = i; }
         fmin = fminf(fmin, s.wmin[w]);
     }
+    double Z = 0.0;
+    if (sampled && m != -INFINITY)
+        for (uint32_t w = 0; w < kSelWaves; ++w)
+            if (s.wzm[w] != -INFINITY) Z += s.wzs[w] * (double)__builtin_amdgcn_exp2f((s.wzm[w] - m) * kLog2e);
     __syncthreads();
 
     RowReport rep = {};
@@ -617,14 +662,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a, uint2* __r
         rep.shortlist = 1;
         rep.cut = 1;
     } else {
-        // 2. Z = sum_t exp(max_t - m) * sumexp_t (fp32 exp, double sum)
-        double zl = 0.0;
-        if (m != -INFINITY)
-            for (uint32_t t = tid; t < a.ntile; t += kSelThreads) {
-                const BlockPartial p = parts[t];
-                if (p.max != -INFINITY) zl += (double)(__builtin_amdgcn_exp2f((p.max - m) * kLog2e) * p.sumexp);
-            }
-        const double Z = block_sum<double>(zl, s);
+        // 2. Z = sum over the row of exp(l - m), from the block partials (pass 1)
         rep.total = Z;
         const float* lrow = a.logits + (size_t)b * a.V;
         const uint32_t want = row.want;
@@ -637,26 +675,55 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a, uint2* __r
             general = false;
         } else if (!general) {
             // ---- shortlist path ----
-            // tau: lower edge of the 22-bit key bin holding the want-th largest block maximum
+            // tau: a lower bound of the want-th largest block maximum, hence of the want-th
+            // largest logit. First try one histogram of the block maxima over value bins of
+            // width 1/64 below m: with the want-th maximum in bin j (bins counted from m down),
+            // every counted block lies above m - (j + 1) w up to rounding far below one bin, so
+            // m - (j + 2) w is a safe bound. It needs |m| <= 1024 (value rounding << w) and the
+            // want-th maximum within kTauSpan of m; otherwise the exact 22-bit key bound (two
+            // 11-bit histogram levels).
             uint32_t tau = 0u;
             if (a.ntile > want) {
-                uint32_t prefix = 0, mask = 0, rem = want;
-                for (int lv = 0; lv < 2; ++lv) {
-                    const uint32_t sh = (lv == 0) ? 21u : 10u;
+                constexpr float kTauSpan = 32.0f;
+                constexpr float kTauInv = (float)kBins / kTauSpan;
+                bool found = false;
+                if (fabsf(m) <= 1024.0f) {
                     for (uint32_t i = tid; i < kBins; i += kSelThreads) s.hu[i] = 0u;
                     __syncthreads();
                     for (uint32_t t = tid; t < a.ntile; t += kSelThreads) {
-                        const uint32_t k = pkey(t);
-                        if ((k & mask) == prefix) atomicAdd(&s.hu[(k >> sh) & (kBins - 1u)], 1u);
+                        const float v = key_float(pkey(t));
+                        if (v >= m - kTauSpan) {
+                            const uint32_t j = min(kBins - 1u, (uint32_t)((m - v) * kTauInv));
+                            atomicAdd(&s.hu[kBins - 1u - j], 1u);  // hist_cross scans from the top bin
+                        }
                     }
                     __syncthreads();
                     uint32_t bin = 0, above = 0;
-                    hist_cross<uint32_t>(s, kBins, rem, &bin, &above);
-                    rem -= above;
-                    prefix |= bin << sh;
-                    mask |= (kBins - 1u) << sh;
+                    if (hist_cross<uint32_t>(s, kBins, want, &bin, &above)) {
+                        const uint32_t j = kBins - 1u - bin;
+                        tau = float_key(m - (float)(j + 2u) * (kTauSpan / (float)kBins));
+                        found = true;
+                    }
                 }
-                tau = prefix;
+                if (!found) {
+                    uint32_t prefix = 0, mask = 0, rem = want;
+                    for (int lv = 0; lv < 2; ++lv) {
+                        const uint32_t sh = (lv == 0) ? 21u : 10u;
+                        for (uint32_t i = tid; i < kBins; i += kSelThreads) s.hu[i] = 0u;
+                        __syncthreads();
+                        for (uint32_t t = tid; t < a.ntile; t += kSelThreads) {
+                            const uint32_t k = pkey(t);
+                            if ((k & mask) == prefix) atomicAdd(&s.hu[(k >> sh) & (kBins - 1u)], 1u);
+                        }
+                        __syncthreads();
+                        uint32_t bin = 0, above = 0;
+                        hist_cross<uint32_t>(s, kBins, rem, &bin, &above);
+                        rem -= above;
+                        prefix |= bin << sh;
+                        mask |= (kBins - 1u) << sh;
+                    }
+                    tau = prefix;
+                }
             }
             if (tid == 0) { s.bu[3] = 0u; s.bu[4] = 0u; }
             __syncthreads();
@@ -698,33 +765,84 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a, uint2* __r
                 __syncthreads();
                 if (!general) {
                     sort_cand(s, n);
+                    // Nucleus over full-distribution probabilities p = exp(l - m) / Z (:139-151),
+                    // then the draw over q = exp((l - m) / T) (:153-168). Both are computed for
+                    // every shortlist entry; inclusive prefix sums up to the cut are unaffected by
+                    // the entries past it.
                     const uint32_t W = min(want, n);
-                    float li = -INFINITY;
-                    uint32_t idi = 0;
-                    if (tid < W) {
-                        const unsigned long long cv = s.cand[tid];
-                        li = key_float(~(uint32_t)(cv >> 32));
-                        idi = (uint32_t)cv;
+                    uint32_t cut = 0, rank = 0;
+                    double denom = 0.0, r = 0.0;
+                    if (W <= 64u) {
+                        // one wave: shuffle scans and ballots, no barriers
+                        if (wave == 0u) {
+                            float li = -INFINITY;
+                            uint32_t idi = 0;
+                            double pv = 0.0, qv = 0.0;
+                            if (lane < W) {
+                                const unsigned long long cv = s.cand[lane];
+                                li = key_float(~(uint32_t)(cv >> 32));
+                                idi = (uint32_t)cv;
+                                const double dl = (double)li - (double)m;
+                                pv = exp(dl) / Z;
+                                qv = exp(dl / (double)row.temperature);
+                            }
+                            const double runp = wave_incl_scan(pv, lane);
+                            const double runq = wave_incl_scan(qv, lane);
+                            uint32_t ct = W;
+                            if (row.top_p < 1.0f) {
+                                const unsigned long long mk = __ballot(lane < W && runp >= (double)row.top_p);
+                                if (mk) ct = (uint32_t)__ffsll((long long)mk);
+                            }
+                            if (row.top_k > 0 && ct > (uint32_t)row.top_k) ct = (uint32_t)row.top_k;
+                            if (ct < 1u) ct = 1u;
+                            const double dn = __shfl(runq, (int)ct - 1, 64);
+                            const double rr = (double)u * dn;
+                            const unsigned long long mk2 = __ballot(lane < ct && runq >= rr);
+                            const uint32_t rk = mk2 ? (uint32_t)(__ffsll((long long)mk2) - 1) : ct - 1u;
+                            const uint32_t tk = (uint32_t)__shfl((int)idi, (int)rk, 64);
+                            if (lane == 0u) {
+                                s.bu[5] = tk; s.bu[6] = ct; s.bu[7] = rk;
+                                s.bd[1] = dn; s.bd[2] = rr;
+                            }
+                        }
+                        __syncthreads();
+                        token = s.bu[5];
+                        cut = s.bu[6];
+                        rank = s.bu[7];
+                        denom = s.bd[1];
+                        r = s.bd[2];
+                    } else {
+                        float li = -INFINITY;
+                        uint32_t idi = 0;
+                        double pv = 0.0, qv = 0.0;
+                        if (tid < W) {
+                            const unsigned long long cv = s.cand[tid];
+                            li = key_float(~(uint32_t)(cv >> 32));
+                            idi = (uint32_t)cv;
+                            const double dl = (double)li - (double)m;
+                            pv = exp(dl) / Z;
+                            qv = exp(dl / (double)row.temperature);
+                        }
+                        const double runq = block_excl_scan<double>(qv, s, nullptr) + qv;
+                        cut = W;
+                        if (row.top_p < 1.0f) {
+                            const double runp = block_excl_scan<double>(pv, s, nullptr) + pv;
+                            const uint32_t first =
+                                block_min_u((tid < W && runp >= (double)row.top_p) ? tid : 0xFFFFFFFFu, s);
+                            if (first != 0xFFFFFFFFu) cut = first + 1u;
+                        }
+                        if (row.top_k > 0 && cut > (uint32_t)row.top_k) cut = (uint32_t)row.top_k;
+                        if (cut < 1u) cut = 1u;
+                        if (tid == cut - 1u) s.bd[1] = runq;
+                        __syncthreads();
+                        denom = s.bd[1];
+                        r = (double)u * denom;
+                        const uint32_t pick = block_min_u((tid < cut && runq >= r) ? tid : 0xFFFFFFFFu, s);
+                        rank = (pick == 0xFFFFFFFFu) ? cut - 1u : pick;
+                        if (tid == rank) s.bu[5] = idi;
+                        __syncthreads();
+                        token = s.bu[5];
                     }
-                    uint32_t cut = W;
-                    if (row.top_p < 1.0f) {
-                        const double p = (tid < W) ? exp((double)li - (double)m) / Z : 0.0;
-                        const double run = block_excl_scan<double>(p, s, nullptr) + p;
-                        const uint32_t first =
-                            block_min_u((tid < W && run >= (double)row.top_p) ? tid : 0xFFFFFFFFu, s);
-                        if (first != 0xFFFFFFFFu) cut = first + 1u;
-                    }
-                    if (row.top_k > 0 && cut > (uint32_t)row.top_k) cut = (uint32_t)row.top_k;
-                    if (cut < 1u) cut = 1u;
-                    const double q = (tid < cut) ? exp(((double)li - (double)m) / (double)row.temperature) : 0.0;
-                    double denom;
-                    const double acc = block_excl_scan<double>(q, s, &denom) + q;
-                    const double r = (double)u * denom;
-                    const uint32_t pick = block_min_u((tid < cut && acc >= r) ? tid : 0xFFFFFFFFu, s);
-                    const uint32_t rank = (pick == 0xFFFFFFFFu) ? cut - 1u : pick;
-                    if (tid == rank) s.bu[5] = idi;
-                    __syncthreads();
-                    token = s.bu[5];
                     rep.cut = cut;
                     rep.rank = rank;
                     rep.denom = denom;
