@@ -55,6 +55,9 @@ def parse():
     ap.add_argument("--cpu-steps", type=int, default=4)
     ap.add_argument("--only", choices=["b1", "b32", "b256"], default=None,
                     help="run one workload only (profiling); prints its own JSON line")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="copy a buffer of the table's size 5 times (a plain copy kernel of known "
+                         "size, to calibrate rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
     return ap.parse_args()
 
 
@@ -180,6 +183,14 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     import torch
+    if a.copy_calibration:
+        src = torch.ones(WEIGHT_BYTES // 4, dtype=torch.int32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": WEIGHT_BYTES, "copies": 5}), flush=True)
+        return
     import synth
     import turbo_decode_tail as T
 
