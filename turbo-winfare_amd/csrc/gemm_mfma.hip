@@ -18,12 +18,10 @@
 //    activation fragment is read from LDS with the same (chunk, word) mapping, and the
 //    activations are stored k-permuted within each octet as (x0, x4, x1, x5, x2, x6, x3, x7)
 //    to match the order the dequant produces halves in.
-//  * Workgroup = 4 M-waves (4 x 64 rows) x NWN N-waves; a wave owns 64 rows x 32*NB columns.
-//    For 64 < B <= 128 one wave per SIMD owns all 128 columns (every weight dequantised once);
-//    above, two N-waves of 128 columns share each 64-row tile.
-//    Weights are prefetched PF groups ahead into registers; activations for group g+1 are
-//    staged through registers into the other half of a double-buffered LDS tile while group g
-//    computes, one barrier per group.
+//  * Workgroup = 4 waves, one 64-row tile each, over a block of 32*NB batch columns
+//    (blockIdx.y: B = 256 runs two column blocks). Weights are prefetched PF groups ahead into
+//    registers; activations for group g+1 are staged through registers into the other half of a
+//    double-buffered LDS tile while group g computes, one barrier per group.
 //  * Epilogue in place on the accumulators: per (column, 64-row tile), lane-local reductions
 //    and one cross-lane exchange give the block partial; logits leave as float4 stores.
 #include <hip/hip_ext.h>
@@ -72,62 +70,85 @@ __device__ inline h8v dequant_word(uint32_t w, h2v s2, h2v b2, h2v b16) {
     return o;
 }
 
-// Softcap for the batched path. For |z/cap| < 9 it uses tanh(x) = sign(x)(1 - 2/(exp(2|x|)+1))
-// with the hardware exp2/rcp (relative error ~1e-6, far below the fp16-dequant error of this
-// path); beyond, tanh rounds to +-1 in fp32, as libm's tanhf does.
-__device__ inline float softcap_fast(float z, float cap) {
-    const float x = z / cap;
-    const float ax = fabsf(x);
-    float t = 1.0f;
-    if (ax < 9.0f) t = 1.0f - 2.0f / (__expf(2.0f * ax) + 1.0f);
+// Softcap for the batched path: x = z / cap through the reciprocal, then
+// tanh(x) = sign(x) (1 - 2 / (exp(2|x|) + 1)) with the hardware exp2 and rcp. For large |x|
+// exp overflows to +inf and rcp(inf) = 0 gives exactly +-1, as libm's tanhf does once
+// |x| > 9. Relative error ~1e-6, far below this path's fp16-dequant error.
+__device__ inline float softcap_fast(float z, float cap, float inv_cap) {
+    const float x = z * inv_cap;
+    const float e = __builtin_amdgcn_exp2f(fabsf(x) * 2.8853900817779268f);  // exp(2|x|)
+    const float t = fmaf(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f);
     return cap * copysignf(t, x);
 }
 
 // Row held in register r of a 32x32 accumulator by a lane with half hl (0/1): 8(r/4) + 4hl + r%4.
 __device__ inline uint32_t acc_row(int r, uint32_t hl) { return 8u * (uint32_t)(r >> 2) + 4u * hl + (uint32_t)(r & 3); }
 
-// OCC = minimum waves per SIMD the register allocation must allow.
-template <int NB, int NWN, int PF, int OCC>
-__global__ __launch_bounds__(256 * NWN, OCC) void k_head_mfma(
+// Scale / bias halves of one (row, group): s, b and 16 b (for the high-nibble slots).
+struct SbHalves {
+    h2v s2, b2, b16;
+};
+__device__ inline SbHalves unpack_sb(uint32_t sc) {
+    const _Float16 sh = (_Float16)bf16_to_f32(sc & 0xFFFFu);
+    const float bf = bf16_to_f32(sc >> 16);
+    SbHalves r;
+    r.s2 = h2v{sh, sh};
+    r.b2 = h2v{(_Float16)bf, (_Float16)bf};
+    r.b16 = h2v{(_Float16)(16.0f * bf), (_Float16)(16.0f * bf)};
+    return r;
+}
+__device__ inline uint32_t word_of(const uint4& w, int j) { return (j == 0) ? w.x : (j == 1) ? w.y : (j == 2) ? w.z : w.w; }
+
+// Workgroup = 4 waves, one 64-row tile each, over a block of NCOL = 32 NB batch columns
+// (blockIdx.y). Two or more independent workgroups share a CU, so one's epilogue overlaps
+// another's main loop and their barriers do not line up.
+// FULL: every column of the block exists (B % NCOL == 0): activation loads need no guard.
+// The main loop runs in rounds of PF groups (G % PF == 0) without branches: loads past the
+// last group are clamped to it and never used, so the compiler's load counters stay exact and
+// the weight prefetch is never drained early. The next k-step's weights are dequantised in
+// the shadow of the current step's MFMAs.
+template <int NB, int PF, int OCC, bool FULL>
+__global__ __launch_bounds__(256, OCC) void k_head_mfma(
     const uint4* __restrict__ Wt, const uint32_t* __restrict__ SBt, const uint16_t* __restrict__ x16,
     uint32_t B, uint32_t D, uint32_t NC, uint32_t G, EpiArgs ep) {
-    constexpr uint32_t NT = 256 * NWN;
-    constexpr uint32_t NCOL = 32 * NB * NWN;
+    constexpr uint32_t NT = 256;
+    constexpr uint32_t NCOL = 32 * NB;
     constexpr uint32_t XP = NCOL * 8;                 // 16-byte activation pieces per group
-    constexpr uint32_t XPT = (XP + NT - 1) / NT;
+    constexpr uint32_t XPT = XP / NT;
+    static_assert(XP % NT == 0, "activation pieces must split evenly over the threads");
     __shared__ __attribute__((aligned(16))) _Float16 lx[2][NCOL * kColHalves];
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    const uint32_t wm = wave & 3u, wn = wave >> 2;
-    const uint32_t tile_raw = blockIdx.x * 4u + wm;
+    const uint32_t cbase = blockIdx.y * NCOL;         // first batch column of this workgroup
+    const uint32_t tile_raw = blockIdx.x * 4u + wave;
     const bool tile_ok = tile_raw < ep.ntile;
     const uint32_t tile = tile_ok ? tile_raw : ep.ntile - 1u;  // clamp loads; skip the epilogue
     const uint32_t hl = lane >> 5, l32 = lane & 31u;
 
     const uint4* wbase = Wt + (size_t)tile * NC * kTileRows + (size_t)hl * kTileRows + l32;
     const uint32_t* sbbase = SBt + (size_t)tile * G * kTileRows + l32;
-    auto wptr = [&](uint32_t g, int mb) { return wbase + (size_t)(2u * g) * kTileRows + 32u * mb; };
+    auto wload = [&](uint32_t g, int mb) { return load_stream(wbase + (size_t)(2u * g) * kTileRows + 32u * mb); };
+    auto sload = [&](uint32_t g, int mb) { return load_stream(sbbase + (size_t)g * kTileRows + 32u * mb); };
 
-    auto load_x = [&](uint32_t g, uint4* xr) {
+    auto load_x = [&](uint32_t g, v4u* xr) {
 #pragma unroll
         for (uint32_t p = 0; p < XPT; ++p) {
             const uint32_t pc = tid + p * NT;
-            uint4 v = make_uint4(0u, 0u, 0u, 0u);
-            if (pc < XP) {
-                const uint32_t n = pc >> 3, o = pc & 7u;
-                if (n < B) v = *reinterpret_cast<const uint4*>(x16 + (size_t)n * D + 64u * g + 8u * o);
+            const uint32_t n = cbase + (pc >> 3), o = pc & 7u;
+            if constexpr (FULL) {
+                xr[p] = *reinterpret_cast<const v4u*>(x16 + (size_t)n * D + 64u * g + 8u * o);
+            } else {
+                v4u v = {0u, 0u, 0u, 0u};
+                if (n < B) v = *reinterpret_cast<const v4u*>(x16 + (size_t)n * D + 64u * g + 8u * o);
+                xr[p] = v;
             }
-            xr[p] = v;
         }
     };
-    auto store_x = [&](uint32_t buf, const uint4* xr) {
+    auto store_x = [&](uint32_t buf, const v4u* xr) {
 #pragma unroll
         for (uint32_t p = 0; p < XPT; ++p) {
             const uint32_t pc = tid + p * NT;
-            if (pc < XP) {
-                const uint32_t n = pc >> 3, o = pc & 7u;
-                *reinterpret_cast<uint4*>(&lx[buf][n * kColHalves + 8u * o]) = xr[p];
-            }
+            *reinterpret_cast<v4u*>(&lx[buf][(pc >> 3) * kColHalves + 8u * (pc & 7u)]) = xr[p];
         }
     };
 
@@ -143,65 +164,69 @@ __global__ __launch_bounds__(256 * NWN, OCC) void k_head_mfma(
     uint32_t sbr[PF][2];
 #pragma unroll
     for (int p = 0; p < PF; ++p) {
-        if ((uint32_t)p < G) {
+        const uint32_t gp = min((uint32_t)p, G - 1u);
 #pragma unroll
-            for (int mb = 0; mb < 2; ++mb) {
-                wr[p][mb] = load_stream(wptr(p, mb));
-                sbr[p][mb] = load_stream(sbbase + (size_t)p * kTileRows + 32u * mb);
-            }
-        }
+        for (int mb = 0; mb < 2; ++mb) { wr[p][mb] = wload(gp, mb); sbr[p][mb] = sload(gp, mb); }
     }
-    uint4 xr[XPT];
+    v4u xr[XPT];
     load_x(0, xr);
     store_x(0, xr);
     __syncthreads();
 
+    h8v acur[2], anext[2];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+        const SbHalves h = unpack_sb(sbr[0][mb]);
+        acur[mb] = dequant_word(wr[0][mb].x, h.s2, h.b2, h.b16);
+    }
     uint32_t buf = 0;
     for (uint32_t g0 = 0; g0 < G; g0 += PF) {
 #pragma unroll
         for (int p = 0; p < PF; ++p) {
             const uint32_t g = g0 + p;
-            if (g < G) {
-                uint4 wc[2];
-                uint32_t sc[2];
+            uint4 wc[2];
+            SbHalves hc[2];
 #pragma unroll
-                for (int mb = 0; mb < 2; ++mb) { wc[mb] = wr[p][mb]; sc[mb] = sbr[p][mb]; }
-                const uint32_t gn = g + PF;
-                if (gn < G) {
+            for (int mb = 0; mb < 2; ++mb) { wc[mb] = wr[p][mb]; hc[mb] = unpack_sb(sbr[p][mb]); }
+            load_x(min(g + 1u, G - 1u), xr);
+            const uint32_t gn = min(g + (uint32_t)PF, G - 1u);
 #pragma unroll
-                    for (int mb = 0; mb < 2; ++mb) {
-                        wr[p][mb] = load_stream(wptr(gn, mb));
-                        sbr[p][mb] = load_stream(sbbase + (size_t)gn * kTileRows + 32u * mb);
+            for (int mb = 0; mb < 2; ++mb) { wr[p][mb] = wload(gn, mb); sbr[p][mb] = sload(gn, mb); }
+            constexpr int kNext = (PF > 1) ? 1 : 0;
+            const int pn = (p + kNext) % PF;         // prefetch slot holding group g + 1
+            const _Float16* lb = &lx[buf][0];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb) {
+                    if (j < 3) {
+                        anext[mb] = dequant_word(word_of(wc[mb], j + 1), hc[mb].s2, hc[mb].b2, hc[mb].b16);
+                    } else {
+                        const SbHalves h = unpack_sb(sbr[pn][mb]);
+                        anext[mb] = dequant_word(wr[pn][mb].x, h.s2, h.b2, h.b16);
                     }
                 }
-                const bool more = g + 1u < G;
-                if (more) load_x(g + 1u, xr);
-                const _Float16* lb = &lx[buf][0];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    h8v a[2];
+                for (int nb = 0; nb < NB; ++nb) {
+                    const uint32_t n = 32u * nb + l32;
+                    const h8v bv = *reinterpret_cast<const h8v*>(lb + n * kColHalves + 32u * hl + 8u * j);
 #pragma unroll
-                    for (int mb = 0; mb < 2; ++mb) {
-                        const _Float16 s = (_Float16)bf16_to_f32(sc[mb] & 0xFFFFu);
-                        const float bfv = bf16_to_f32(sc[mb] >> 16);
-                        const _Float16 b = (_Float16)bfv;
-                        const _Float16 b16 = (_Float16)(16.0f * bfv);
-                        const uint32_t wj = (j == 0) ? wc[mb].x : (j == 1) ? wc[mb].y : (j == 2) ? wc[mb].z : wc[mb].w;
-                        a[mb] = dequant_word(wj, h2v{s, s}, h2v{b, b}, h2v{b16, b16});
-                    }
-#pragma unroll
-                    for (int nb = 0; nb < NB; ++nb) {
-                        const uint32_t n = wn * (32u * NB) + 32u * nb + l32;
-                        const h8v bv = *reinterpret_cast<const h8v*>(lb + n * kColHalves + 32u * hl + 8u * j);
-#pragma unroll
-                        for (int mb = 0; mb < 2; ++mb)
-                            acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mb], bv, acc[mb][nb], 0, 0, 0);
-                    }
+                    for (int mb = 0; mb < 2; ++mb)
+                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(acur[mb], bv, acc[mb][nb], 0, 0, 0);
                 }
-                if (more) store_x(buf ^ 1u, xr);
-                __syncthreads();
-                buf ^= 1u;
+                // one LDS read, one MFMA, then dequant VALU work in the MFMA's shadow
+#pragma unroll
+                for (int i = 0; i < 2 * NB; ++i) {
+                    if (i < NB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, (NB >= 4) ? 5 : (NB == 2 ? 9 : 17), 0);
+                }
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb) acur[mb] = anext[mb];
             }
+            store_x(buf ^ 1u, xr);
+            __syncthreads();
+            buf ^= 1u;
         }
     }
     if (!tile_ok) return;
@@ -209,16 +234,18 @@ __global__ __launch_bounds__(256 * NWN, OCC) void k_head_mfma(
     // ---- epilogue, in place on the accumulators ----
     const uint32_t base = tile * kTileRows;
     const bool vec_ok = (ep.V & 3u) == 0u;  // float4 stores need 16-byte aligned rows
+    const bool full_tile = base + kTileRows <= ep.V;
+    const float inv_cap = (ep.cap > 0.0f) ? 1.0f / ep.cap : 0.0f;
     // One column block at a time, indexed at compile time so the accumulators stay in registers.
     auto column = [&]<int nb>() {
-        const uint32_t bcol = wn * (32u * NB) + 32u * nb + l32;
+        const uint32_t bcol = cbase + 32u * nb + l32;
         const bool col_ok = bcol < B;
         const uint32_t bq = col_ok ? bcol : 0u;
         if (ep.cap > 0.0f) {
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[mb][nb][r] = softcap_fast(acc[mb][nb][r], ep.cap);
+                for (int r = 0; r < 16; ++r) acc[mb][nb][r] = softcap_fast(acc[mb][nb][r], ep.cap, inv_cap);
         }
         if (col_ok && ep.rows[bq].has_mods) {
             const DevRow row = ep.rows[bq];
@@ -254,11 +281,24 @@ __global__ __launch_bounds__(256 * NWN, OCC) void k_head_mfma(
                     }
             }
         }
-        uint32_t ban0 = 0u, ban1 = 0u;
         if (col_ok && ep.ban) {
             const uint32_t* bw = ep.ban + (size_t)bq * ep.ban_stride + (base >> 5);
-            ban0 = bw[0];
-            if (base + 32u < ep.V) ban1 = bw[1];
+            const uint32_t ban0 = bw[0];
+            const uint32_t ban1 = (base + 32u < ep.V) ? bw[1] : 0u;
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t rr = 32u * mb + acc_row(r, hl);
+                    if ((((mb == 0) ? ban0 : ban1) >> (rr & 31u)) & 1u) acc[mb][nb][r] = -INFINITY;
+                }
+        }
+        if (!full_tile) {
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (base + 32u * mb + acc_row(r, hl) >= ep.V) acc[mb][nb][r] = -INFINITY;
         }
         float bmax = -INFINITY, bmin = INFINITY;
         uint32_t barg = 0xFFFFFFFFu;
@@ -266,12 +306,8 @@ __global__ __launch_bounds__(256 * NWN, OCC) void k_head_mfma(
         for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const uint32_t rr = 32u * mb + acc_row(r, hl);
-                float z = acc[mb][nb][r];
-                if ((((mb == 0) ? ban0 : ban1) >> (rr & 31u)) & 1u) z = -INFINITY;
-                if (base + rr >= ep.V) z = -INFINITY;
-                acc[mb][nb][r] = z;
-                if (z > bmax) { bmax = z; barg = base + rr; }  // rows visited in increasing order
+                const float z = acc[mb][nb][r];
+                if (z > bmax) { bmax = z; barg = base + 32u * mb + acc_row(r, hl); }  // rows in increasing order
                 if (z != -INFINITY) bmin = fminf(bmin, z);
             }
         bmin = fminf(bmin, __shfl_xor(bmin, 32, 64));
@@ -298,10 +334,12 @@ __global__ __launch_bounds__(256 * NWN, OCC) void k_head_mfma(
         if (om > bmax || (om == bmax && oa < barg)) { bmax = om; barg = oa; }
         float se = 0.0f;
         if (bmax != -INFINITY) {
+            const float mb2 = bmax * 1.4426950408889634f;
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) se += __expf(acc[mb][nb][r] - bmax);
+                for (int r = 0; r < 16; ++r)
+                    se += __builtin_amdgcn_exp2f(fmaf(acc[mb][nb][r], 1.4426950408889634f, -mb2));
         }
         se += __shfl_xor(se, 32, 64);
         if (col_ok && hl == 0u) {
@@ -320,16 +358,25 @@ __global__ __launch_bounds__(256 * NWN, OCC) void k_head_mfma(
 
 void launch_head_mfma(const Head& h, int batch, const EpiArgs& ep, hipStream_t st, hipEvent_t ev0,
                       hipEvent_t ev1) {
-    const unsigned grid = (h.ntile + 3u) / 4u;
     const uint32_t B = (uint32_t)batch;
-#define TDT_LAUNCH(NB, NWN, PF, OCC)                                                           \
-    hipExtLaunchKernelGGL((k_head_mfma<NB, NWN, PF, OCC>), dim3(grid), dim3(256 * NWN), 0, st, ev0, \
-                          ev1, 0, h.Wt, h.SBt, h.x16, B, h.D, h.NC, h.G, ep)
-    if (B <= 32) TDT_LAUNCH(1, 1, 4, 4);
-    else if (B <= 64) TDT_LAUNCH(2, 1, 4, 3);
-    else if (B <= 128) TDT_LAUNCH(4, 1, 2, 1);
-    else if (B <= 256) TDT_LAUNCH(4, 2, 2, 2);
-    else throw std::runtime_error("MFMA head supports batch <= 256");
+    if (B > 256u) throw std::runtime_error("MFMA head supports batch <= 256");
+    const int nb = (B <= 32u) ? 1 : (B <= 64u) ? 2 : 4;
+    const uint32_t ncol = 32u * (uint32_t)nb;
+    const dim3 grid((h.ntile + 3u) / 4u, (B + ncol - 1u) / ncol);
+    const bool full = (B % ncol) == 0u;
+    const bool pf2 = (h.G % 2u) == 0u;
+#define TDT_LAUNCH(NB, PF, OCC, FULL)                                                              \
+    hipExtLaunchKernelGGL((k_head_mfma<NB, PF, OCC, FULL>), grid, dim3(256), 0, st, ev0, ev1, 0, h.Wt, \
+                          h.SBt, h.x16, B, h.D, h.NC, h.G, ep)
+#define TDT_PICK(NB, OCC)                                                    \
+    do {                                                                     \
+        if (pf2) { if (full) TDT_LAUNCH(NB, 2, OCC, true); else TDT_LAUNCH(NB, 2, OCC, false); } \
+        else { if (full) TDT_LAUNCH(NB, 1, OCC, true); else TDT_LAUNCH(NB, 1, OCC, false); }     \
+    } while (0)
+    if (nb == 1) TDT_PICK(1, 4);
+    else if (nb == 2) TDT_PICK(2, 3);
+    else TDT_PICK(4, 2);
+#undef TDT_PICK
 #undef TDT_LAUNCH
     check_hip(hipGetLastError(), "head (MFMA)");
 }
