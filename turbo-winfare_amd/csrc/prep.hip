@@ -96,17 +96,26 @@ __device__ void prep_row(const PrepArgs& a, uint32_t b, float* sx) {
     __shared__ double red[kPrepWaves];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t D = a.D;
-    for (uint32_t i = tid; i < D; i += kPrepThreads) {
-        float v;
-        if (a.dtype == 1) v = bf16_to_f32(reinterpret_cast<const uint16_t*>(a.hidden)[(size_t)b * D + i]);
-        else v = reinterpret_cast<const float*>(a.hidden)[(size_t)b * D + i];
-        sx[i] = v;
+    // hidden and norm weight for this thread's elements, loaded together (one round trip)
+    constexpr uint32_t kPer = 8;  // D <= 8192 = kPer * kPrepThreads
+    float xv[kPer], gv[kPer];
+#pragma unroll
+    for (uint32_t k = 0; k < kPer; ++k) {
+        const uint32_t i = tid + k * kPrepThreads;
+        float v = 0.0f, gw = 1.0f;
+        if (i < D) {
+            if (a.dtype == 1) v = bf16_to_f32(reinterpret_cast<const uint16_t*>(a.hidden)[(size_t)b * D + i]);
+            else v = reinterpret_cast<const float*>(a.hidden)[(size_t)b * D + i];
+            if (a.gamma) gw = bf16_to_f32(a.gamma[i]);
+        }
+        xv[k] = v;
+        gv[k] = gw;
     }
-    __syncthreads();
     if (!a.normed) {
         // src/cpu_reference.cpp:44-46: double sum of squares, float mean + eps, 1/sqrt.
         double acc = 0.0;
-        for (uint32_t i = tid; i < D; i += kPrepThreads) acc += (double)sx[i] * (double)sx[i];
+#pragma unroll
+        for (uint32_t k = 0; k < kPer; ++k) acc += (double)xv[k] * (double)xv[k];
         acc = wave_sum_d(acc);
         if (lane == 0) red[wave] = acc;
         __syncthreads();
@@ -117,13 +126,19 @@ __device__ void prep_row(const PrepArgs& a, uint32_t b, float* sx) {
         // float, which is exact for sqrt and division (53 >= 2 * 24 + 2 bits).
         const float sq = (float)sqrt((double)(ms + a.eps));
         const float inv = (float)(1.0 / (double)sq);
-        for (uint32_t i = tid; i < D; i += kPrepThreads) {
-            float v = sx[i] * inv;
-            if (a.gamma) v = v * bf16_to_f32(a.gamma[i]);
-            sx[i] = v;
+#pragma unroll
+        for (uint32_t k = 0; k < kPer; ++k) {
+            float v = xv[k] * inv;
+            if (a.gamma) v = v * gv[k];
+            xv[k] = v;
         }
-        __syncthreads();
     }
+#pragma unroll
+    for (uint32_t k = 0; k < kPer; ++k) {
+        const uint32_t i = tid + k * kPrepThreads;
+        if (i < D) sx[i] = xv[k];
+    }
+    __syncthreads();
     if (a.xn)
         for (uint32_t i = tid; i < D; i += kPrepThreads) a.xn[(size_t)b * D + i] = sx[i];
     if (a.path == 0) {
