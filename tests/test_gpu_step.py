@@ -312,3 +312,25 @@ def test_digit_path_modifiers_bit_exact(head):
         bad = np.nonzero(logits[b].view(np.uint32) != want.view(np.uint32))[0]
         assert bad.size == 0, (b, int(bad.size), [(int(i), float(logits[b, i]), float(want[i])) for i in bad[:6]])
     check_sampler_on_gpu_logits(rows, toks, logits, [T.row_uniform(r) for r in rows])
+
+
+def test_full_vocab_rows_split_over_workgroups(head):
+    """Small batches split each full-vocabulary row over several workgroups (histogram and
+    gather per slice, the last workgroup draws). Two calls in a row move a degenerate row (every
+    id -inf) so that no state of the first call leaks into the second: degenerate rows report
+    0xFFFFFFFF and every other row matches the oracle sampler."""
+    h, _ = head
+    Bn = 4
+    cfgs = [(1.0, 0.9), (0.7, 0.95), (1.3, 0.5), (0.9, 0.99)]
+    rows = [T.row_default(temperature=t, top_p=p, top_k=0, seed=600 + i, counter=5,
+                          flags=T.TURBO_ROW_FULL_VOCAB) for i, (t, p) in enumerate(cfgs)]
+    us = [T.row_uniform(r) for r in rows]
+    for call, dead in enumerate((1, 2)):
+        base = (synth.normal(SEED + call, 83, Bn * V).reshape(Bn, V) * 3).astype(np.float32)
+        base[dead] = -np.inf
+        toks, after, rep = sample_given(h, base, rows)
+        assert int(toks[dead]) == 0xFFFFFFFF, (call, int(toks[dead]))
+        live = [b for b in range(Bn) if b != dead]
+        check_sampler_on_gpu_logits([rows[b] for b in live], toks[live], base[live], [us[b] for b in live])
+        paths = rep.view(np.uint32)[:, 5]
+        assert all(paths[b] == 2 for b in live), paths

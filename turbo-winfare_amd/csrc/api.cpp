@@ -155,6 +155,10 @@ void free_head(Head& h) {
     dfree(h.hcount);
     dfree(h.hbits);
     dfree(h.list_scratch);
+    dfree(h.fv_part);
+    dfree(h.fv_merged);
+    dfree(h.fv_cand);
+    dfree(h.fv_state);
     if (h.ring_host) (void)hipHostFree(h.ring_host);
     for (int i = 0; i < Head::kRing; ++i)
         if (h.ring_ev[i]) (void)hipEventDestroy(h.ring_ev[i]);
@@ -310,7 +314,7 @@ int run_rows(HandleBox& bx, const TurboStepInputs* in, const TurboStepOutputs* o
         throw std::runtime_error("ban_stride must be at least ceil(vocab / 32) words");
 
     tdt::DevRow rows[kMaxBatch];
-    bool all_greedy = true, any_mods = false;
+    bool all_greedy = true, any_mods = false, any_fv = false;
     for (int b = 0; b < B; ++b) {
         const TurboSamplingRow& r = in->rows[b];
         std::string why;
@@ -321,6 +325,7 @@ int run_rows(HandleBox& bx, const TurboStepInputs* in, const TurboStepOutputs* o
         any_mods = any_mods || mods != 0u;
         all_greedy = all_greedy && r.temperature <= 0.0f;
         rows[b] = make_devrow(h, r, mods);
+        any_fv = any_fv || (rows[b].temperature > 0.0f && rows[b].want >= h.V);
     }
     uint32_t P = 2;
     if (has_bias) P = tdt::modtable_sort_size(h, in->bias_stride);
@@ -376,7 +381,7 @@ int run_rows(HandleBox& bx, const TurboStepInputs* in, const TurboStepOutputs* o
     sa.hcount = h.hcount;
     sa.hbits = h.hbits;
     sa.hbw = h.hbw;
-    tdt::launch_select(h, B, sa, h.stream);
+    tdt::launch_select(h, B, sa, any_fv, h.stream);
     return 1;
 }
 
@@ -494,6 +499,12 @@ TURBO_DT_API void* turbo_lmhead_create(const TurboLMHeadDesc* d) {
         check_hip(hipMemset(h.hcount, 0, MB * h.V * sizeof(uint32_t)), "clear history counts");
         check_hip(hipMemset(h.hbits, 0, MB * h.hbw * sizeof(uint32_t)), "clear history bitmap");
         h.list_scratch = dalloc<uint2>(MB * h.V, "alloc list scratch");
+        h.fv_part = dalloc<unsigned long long>((size_t)tdt::kFvMaxBatch * tdt::kFvSlices * 2u * tdt::kFvBins,
+                                               "alloc select slice histograms");
+        h.fv_merged = dalloc<unsigned long long>((size_t)tdt::kFvMaxBatch * 2u * tdt::kFvBins, "alloc select histograms");
+        h.fv_cand = dalloc<unsigned long long>((size_t)tdt::kFvMaxBatch * tdt::kFvCandCap, "alloc select candidates");
+        h.fv_state = dalloc<unsigned char>((size_t)tdt::kFvMaxBatch * tdt::kFvStateBytes, "alloc select state");
+        check_hip(hipMemset(h.fv_state, 0, (size_t)tdt::kFvMaxBatch * tdt::kFvStateBytes), "clear select state");
         check_hip(hipHostMalloc(reinterpret_cast<void**>(&h.ring_host),
                                 sizeof(tdt::DevRow) * MB * Head::kRing,
                                 hipHostMallocMapped | hipHostMallocCoherent),
@@ -664,7 +675,7 @@ TURBO_DT_API int turbo_lmhead_greedy(void* handle, const void* x, int x_dtype, i
     sa.partials = h.partials;
     sa.rows = h.rows;
     sa.tokens = tokens;
-    tdt::launch_select(h, batch, sa, h.stream);
+    tdt::launch_select(h, batch, sa, false, h.stream);
     return 1;
     API_CATCH(0)
 }

@@ -55,6 +55,10 @@ struct Head {
     uint32_t* mod_count = nullptr;     // [max_batch]
     uint32_t* block_start = nullptr;   // [max_batch][ntile + 1]
     void* list_scratch = nullptr;      // [max_batch][V] uint2 compaction lists (select)
+    unsigned long long* fv_part = nullptr;    // [kFvMaxBatch][kFvSlices][2][kFvBins]
+    unsigned long long* fv_merged = nullptr;  // [kFvMaxBatch][2][kFvBins]
+    unsigned long long* fv_cand = nullptr;    // [kFvMaxBatch][kFvCandCap]
+    void* fv_state = nullptr;                 // [kFvMaxBatch] x kFvStateBytes
 
     // Host staging ring for DevRow uploads (pinned).
     static constexpr int kRing = 8;
@@ -164,8 +168,20 @@ struct SelectArgs {
     uint32_t* hcount;
     uint32_t* hbits;
     uint32_t hbw;
+    // multi-workgroup full-vocabulary path (null fv_part: one workgroup per row)
+    unsigned long long* fv_part;    // [B][kFvSlices][2][kFvBins] slice histograms
+    unsigned long long* fv_merged;  // [B][2][kFvBins] merged histograms
+    unsigned long long* fv_cand;    // [B][kFvCandCap] gathered candidates
+    void* fv_state;                 // [B] x kFvStateBytes per-row plan and counters
 };
-void launch_select(const Head& h, int batch, const SelectArgs& a, hipStream_t st);
+// Small batches split each full-vocabulary row's two passes over kFvSlices workgroups.
+constexpr uint32_t kFvMaxBatch = 64;
+constexpr uint32_t kFvSlices = 16;
+constexpr uint32_t kFvBins = 2048;
+constexpr uint32_t kFvCandCap = 8192;
+constexpr size_t kFvStateBytes = 128;
+// any_fv: some row takes the full-vocabulary value path (sampled, shortlist lifted).
+void launch_select(const Head& h, int batch, const SelectArgs& a, bool any_fv, hipStream_t st);
 
 // misc.hip
 void launch_softcap(float* z, size_t n, float cap, hipStream_t st);

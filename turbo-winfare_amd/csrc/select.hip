@@ -211,6 +211,24 @@ __device__ inline void sort_cand(SelShared& s, uint32_t n) {
     block_sort_u64<kSelThreads>(s.cand, P);
 }
 
+// Stream compaction with one LDS atomic per wave: the active lanes with pred get consecutive
+// slots (in lane order) of dst through *counter; slots past cap are counted but not stored.
+__device__ __attribute__((always_inline)) inline void wave_append(uint32_t* counter, bool pred, unsigned long long key,
+                                   unsigned long long* dst, uint32_t cap) {
+    const unsigned long long mask = __ballot(pred);
+    if (mask == 0ull) return;
+    const uint32_t lane = threadIdx.x & 63u;
+    const int leader = __ffsll((long long)mask) - 1;
+    uint32_t base = 0u;
+    if ((int)lane == leader) base = atomicAdd(counter, (uint32_t)__popcll(mask));
+    base = (uint32_t)__shfl((int)base, leader, 64);
+    if (pred) {
+        const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+        if (base + rank < cap) dst[base + rank] = key;
+    }
+}
+
 // Visits every (value, index) of a row with kInflight independent loads per thread in flight.
 template <class F>
 __device__ inline void row_pass(const float* l, uint32_t V, F&& f) {
@@ -480,17 +498,26 @@ __device__ uint32_t list_bin_start(SelShared& s, const RowCtx& c, uint32_t n, ui
     return first == 0xFFFFFFFFu ? n : first;
 }
 
-// Nucleus over the full distribution, then the temperature draw over the survivors. Returns 1
-// with *token, 0 when a bin is too large to gather (the caller uses the radix fallback).
-__device__ int full_vocab_value_path(SelShared& s, const RowCtx& c, float top_p, float u,
-                                     uint32_t first_id, uint32_t* token, double* denom_out,
-                                     double* r_out) {
-    const uint32_t tid = threadIdx.x;
+// ---- full-vocabulary nucleus over value bins ------------------------------------------------
+// Pieces shared by the one-workgroup path (full_vocab_value_path) and the multi-workgroup path
+// of small batches (k_fv_hist, k_select, k_fv_gather, k_fv_finish): histogram, plan, gather, finish.
+
+// Bins the finish needs: the nucleus bin cb and the range [dlo, dhi] the draw can land in.
+struct FvPlan {
+    uint32_t cb, dlo, dhi, u_zero;  // u_zero: u = 0 picks the first element in sorted order
+    double A;                       // survivor weight (temperature) of the bins above cb
+    double target_w, wabove;        // T = 1 nucleus target, and the T = 1 weight above cb
+};
+
+__device__ inline bool same_weights(const RowCtx& c) { return kLog2e / c.T == kLog2e; }
+
+// Value-bin weight histograms (T = 1 in vm, temperature T in vq) of elements [beg, end).
+__device__ __attribute__((always_inline)) inline void fv_hist(SelShared& s, const RowCtx& c, uint32_t beg, uint32_t end) {
     const float kq = kLog2e / c.T;
-    const bool same = (kq == kLog2e);  // T = 1: one weighting serves nucleus and draw
-    for (uint32_t i = tid; i < kVBins; i += kSelThreads) { s.vm[i] = 0ull; s.vq[i] = 0ull; }
+    const bool same = same_weights(c);  // T = 1: one weighting serves nucleus and draw
+    for (uint32_t i = threadIdx.x; i < kVBins; i += kSelThreads) { s.vm[i] = 0ull; s.vq[i] = 0ull; }
     __syncthreads();
-    row_pass(c.l, c.V, [&](float v, uint32_t) {
+    row_pass(c.l + beg, end - beg, [&](float v, uint32_t) {
         if (v == -INFINITY) return;
         const uint32_t b = vbin(c, v);
         const float d = v - c.m;
@@ -498,7 +525,11 @@ __device__ int full_vocab_value_path(SelShared& s, const RowCtx& c, float top_p,
         if (!same) atomicAdd(&s.vq[b], to_fx(__builtin_amdgcn_exp2f(d * kq)));
     });
     __syncthreads();
-    const unsigned long long* hq = same ? s.vm : s.vq;
+}
+
+// From complete histograms in s.vm / s.vq: the nucleus bin and the draw range.
+__device__ void fv_plan(SelShared& s, const RowCtx& c, float top_p, float u, FvPlan* P) {
+    const unsigned long long* hq = same_weights(c) ? s.vm : s.vq;
     uint32_t bb;
     // nucleus bin: where the T = 1 weight reaches top_p of the row total
     uint32_t cb = kVBins;
@@ -513,53 +544,71 @@ __device__ int full_vocab_value_path(SelShared& s, const RowCtx& c, float top_p,
     double A;
     (void)scan_cross(s, hq, cb, INFINITY, &bb, &A);
     const double Bq = (cb < kVBins) ? (double)hq[cb] / kFx : 0.0;
-    if (!(u > 0.0f)) {  // u = 0: the first element in sorted order
-        *token = first_id;
-        *denom_out = A;
-        *r_out = 0.0;
-        return 1;
-    }
+    P->cb = cb;
+    P->A = A;
+    P->target_w = target_w;
+    P->wabove = wabove;
+    P->u_zero = (u > 0.0f) ? 0u : 1u;
+    P->dlo = P->dhi = cb;
+    if (P->u_zero) return;
     const uint32_t lim = (cb < kVBins) ? cb + 1u : kVBins;
     uint32_t dlo = cb, dhi = cb;
     double ab;
     if (!scan_cross(s, hq, lim, (double)u * A, &dlo, &ab)) dlo = lim - 1u;
     if (!scan_cross(s, hq, lim, (double)u * (A + Bq), &dhi, &ab)) dhi = lim - 1u;
-    // gather {cb} and [dlo, dhi]
-    if (tid == 0) s.bu[2] = 0u;
+    P->dlo = dlo;
+    P->dhi = dhi;
+}
+
+__device__ inline bool fv_wanted(const RowCtx& c, const FvPlan& P, float v) {
+    const uint32_t b = vbin(c, v);
+    return b == P.cb || (b >= P.dlo && b <= P.dhi);
+}
+
+// Appends the elements of [beg, end) in the planned bins to s.cand, counting in s.bu[2]
+// (the count may exceed kCandCap; only the first kCandCap are stored).
+__device__ __attribute__((always_inline)) inline void fv_gather(SelShared& s, const RowCtx& c, const FvPlan& P, uint32_t beg, uint32_t end) {
+    if (threadIdx.x == 0) s.bu[2] = 0u;
     __syncthreads();
-    row_pass(c.l, c.V, [&](float v, uint32_t i) {
-        const uint32_t b = vbin(c, v);
-        if (b != cb && (b < dlo || b > dhi)) return;
-        const uint32_t slot = atomicAdd(&s.bu[2], 1u);
-        if (slot < kCandCap) s.cand[slot] = ((unsigned long long)(~float_key(v)) << 32) | i;
+    row_pass(c.l + beg, end - beg, [&](float v, uint32_t i) {
+        wave_append(&s.bu[2], fv_wanted(c, P, v), ((unsigned long long)(~float_key(v)) << 32) | (beg + i),
+                    s.cand, kCandCap);
     });
     __syncthreads();
-    const uint32_t n = s.bu[2];
-    __syncthreads();
+}
+
+// From the n gathered candidates in s.cand (unsorted) and the histograms in s.vm / s.vq: the
+// nucleus cut inside bin cb and the temperature draw. Returns 1 with *token, 0 when rounding
+// put the draw outside the gathered bins (the caller falls back to the radix path).
+__device__ int fv_finish(SelShared& s, const RowCtx& c, const FvPlan& P, uint32_t n, float u,
+                         uint32_t* token, double* denom_out, double* r_out) {
+    const float kq = kLog2e / c.T;
+    const unsigned long long* hq = same_weights(c) ? s.vm : s.vq;
     if (n > kCandCap || n == 0u) return 0;
     sort_cand(s, n);
+    const uint32_t cb = P.cb;
     // nucleus cut inside bin cb (its elements are the list's last block)
-    double denom = A;
+    double denom = P.A;
     uint32_t cstart = n, ecut = n - 1u;
     if (cb < kVBins) {
         cstart = list_bin_start(s, c, n, cb);
         if (cstart >= n) return 0;
-        ecut = list_cross(s, c, cstart, n - 1u, kLog2e, target_w - wabove, nullptr);
+        ecut = list_cross(s, c, cstart, n - 1u, kLog2e, P.target_w - P.wabove, nullptr);
         double qin;
         (void)list_cross(s, c, cstart, ecut, kq, INFINITY, &qin);
-        denom = A + qin;
+        denom = P.A + qin;
     }
     const double r = (double)u * denom;
     *denom_out = denom;
     *r_out = r;
     uint32_t e;
-    if (cb < kVBins && r > A) {
-        e = list_cross(s, c, cstart, ecut, kq, r - A, nullptr);
+    if (cb < kVBins && r > P.A) {
+        e = list_cross(s, c, cstart, ecut, kq, r - P.A, nullptr);
     } else {
         uint32_t db;
         double dab;
         if (!scan_cross(s, hq, cb, r, &db, &dab)) return 0;
-        if (db < dlo || db > dhi) return 0;  // outside the gathered range (rounding)
+        if (db < P.dlo || db > P.dhi) return 0;  // outside the gathered range (rounding)
         const uint32_t dstart = list_bin_start(s, c, n, db);
         const uint32_t dend = list_bin_start(s, c, n, db + 1u);
         if (dstart >= dend) return 0;
@@ -568,6 +617,223 @@ __device__ int full_vocab_value_path(SelShared& s, const RowCtx& c, float top_p,
     *token = (uint32_t)s.cand[e];
     __syncthreads();
     return 1;
+}
+
+// Nucleus over the full distribution, then the temperature draw over the survivors, in one
+// workgroup. Returns 1 with *token, 0 when a bin is too large to gather (radix fallback).
+__device__ __attribute__((always_inline)) inline int full_vocab_value_path(SelShared& s, const RowCtx& c, float top_p, float u,
+                                     uint32_t first_id, uint32_t* token, double* denom_out,
+                                     double* r_out) {
+    fv_hist(s, c, 0u, c.V);
+    FvPlan P;
+    fv_plan(s, c, top_p, u, &P);
+    if (P.u_zero) {
+        *token = first_id;
+        *denom_out = P.A;
+        *r_out = 0.0;
+        return 1;
+    }
+    fv_gather(s, c, P, 0u, c.V);
+    const uint32_t n = s.bu[2];
+    __syncthreads();
+    return fv_finish(s, c, P, n, u, token, denom_out, r_out);
+}
+
+// Radix fallback over the whole row: shortlist bound, nucleus, then the draw.
+__device__ void radix_select(SelShared& s, const RowCtx& c, const DevRow& row, float u, uint32_t want,
+                             double Z, uint32_t arg, uint32_t* token, RowReport* rep) {
+    uint32_t kx, ix;
+    PSet s0 = {0, 0u, 0u};
+    if (want < c.V && find_cross(s, c, s0, 0, (double)want, &kx, &ix)) s0 = PSet{1, kx, ix};
+    PSet s1 = s0;
+    if (row.top_p < 1.0f && find_cross(s, c, s0, 1, (double)row.top_p * Z, &kx, &ix))
+        s1 = PSet{1, kx, ix};
+    double dl = 0.0;
+    row_pass(c.l, c.V, [&](float v, uint32_t i) {
+        if (s1.has(float_key(v), i)) dl += (double)weight_f(c, v, 2);
+    });
+    const double tot = block_sum<double>(dl, s);
+    const double r = (double)u * tot;
+    if (!(r > 0.0)) *token = arg;
+    else if (find_cross(s, c, s1, 2, r, &kx, &ix)) *token = ix;
+    else *token = s1.bounded ? s1.ib : arg;
+    rep->denom = tot;
+    rep->r = r;
+    rep->path = 4;
+}
+
+// Value-bin context of a row from its maximum and finite minimum.
+__device__ inline RowCtx make_ctx(uint32_t V, const float* l, float m, float fmin, float T, uint2* list) {
+    RowCtx c;
+    c.V = V;
+    c.l = l;
+    c.m = m;
+    c.T = T;
+    c.list = list;
+    const float span = 48.0f * fmaxf(1.0f, T);
+    const float lo = fmaxf(fmin, m - span);
+    c.inv_w = (m > lo) ? (float)kVBins / (m - lo) : 0.0f;
+    return c;
+}
+
+// Row report and token, and the history append (src/runner.cpp:878), by thread 0.
+__device__ inline void write_row(const SelectArgs& a, uint32_t b, uint32_t token, const RowReport& rep) {
+    if (threadIdx.x != 0) return;
+    a.tokens[b] = token;
+    if (a.report) reinterpret_cast<RowReport*>(a.report)[b] = rep;
+    if (a.history && a.hist_len && token != 0xFFFFFFFFu) {
+        const uint32_t len = a.hist_len[b];
+        if (len < a.hist_stride) {
+            a.history[(size_t)b * a.hist_stride + len] = token;
+            a.hist_len[b] = len + 1u;
+        }
+    }
+}
+
+// Rows that take the full-vocabulary value path: sampled, with the shortlist lifted.
+__device__ inline bool is_fv_row(const DevRow& row, uint32_t V) { return row.temperature > 0.0f && row.want >= V; }
+
+// Block-wide maximum and finite minimum of a row's block partials.
+__device__ void partial_max_min(SelShared& s, const BlockPartial* parts, uint32_t ntile, float* m_out, float* fmin_out) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    float bm = -INFINITY, bmin = INFINITY;
+    for (uint32_t t = tid; t < ntile; t += kSelThreads) {
+        const BlockPartial p = parts[t];
+        bm = fmaxf(bm, p.max);
+        bmin = fminf(bmin, p.minf);
+    }
+    bm = wave_max(bm);
+    bmin = wave_min(bmin);
+    if (lane == 0) { s.wmax[wave] = bm; s.wmin[wave] = bmin; }
+    __syncthreads();
+    float m = s.wmax[0], fmin = s.wmin[0];
+    for (uint32_t w = 1; w < kSelWaves; ++w) { m = fmaxf(m, s.wmax[w]); fmin = fminf(fmin, s.wmin[w]); }
+    __syncthreads();
+    *m_out = m;
+    *fmin_out = fmin;
+}
+
+// Slice [beg, end) of a row for workgroup k of S; slices are multiples of 4 elements.
+__device__ inline void fv_slice(uint32_t V, uint32_t S, uint32_t k, uint32_t* beg, uint32_t* end) {
+    const uint32_t len = ((V + S - 1u) / S + 3u) & ~3u;
+    *beg = min(k * len, V);
+    *end = min(*beg + len, V);
+}
+
+// Per-row state of the multi-workgroup path, written by k_select, read by k_fv_gather / k_fv_finish.
+struct FvRowState {
+    FvPlan plan;
+    float m, fmin, T, u, top_p;
+    uint32_t arg, want, active, ncand, overflow;
+    double Z;
+};
+static_assert(sizeof(FvRowState) <= kFvStateBytes, "per-row state must fit its slot");
+static_assert(kFvBins == kVBins && kFvCandCap == kCandCap, "host sizes must match the kernels'");
+
+__device__ inline FvRowState* fv_state_of(const SelectArgs& a, uint32_t b) {
+    return reinterpret_cast<FvRowState*>(reinterpret_cast<char*>(a.fv_state) + (size_t)b * kFvStateBytes);
+}
+
+// Slice histograms of the full-vocabulary rows: workgroup (k, b) bins slice k of row b.
+__global__ __launch_bounds__(kSelThreads) void k_fv_hist(SelectArgs a) {
+    __shared__ SelShared s;
+    const uint32_t k = blockIdx.x, b = blockIdx.y;
+    const DevRow row = a.rows[b];
+    if (!is_fv_row(row, a.V)) return;
+    float m, fmin;
+    partial_max_min(s, a.partials + (size_t)b * a.ntile, a.ntile, &m, &fmin);
+    if (m == -INFINITY) return;  // degenerate row: k_select reports it
+    const RowCtx c = make_ctx(a.V, a.logits + (size_t)b * a.V, m, fmin, row.temperature, nullptr);
+    uint32_t beg, end;
+    fv_slice(a.V, kFvSlices, k, &beg, &end);
+    fv_hist(s, c, beg, end);
+    unsigned long long* dst = a.fv_part + ((size_t)b * kFvSlices + k) * 2u * kVBins;
+    for (uint32_t i = threadIdx.x; i < kVBins; i += kSelThreads) {
+        dst[i] = s.vm[i];
+        dst[kVBins + i] = s.vq[i];
+    }
+}
+
+// Gather of the planned bins, slice k of row b, into the row's global candidate list.
+__global__ __launch_bounds__(kSelThreads) void k_fv_gather(SelectArgs a, uint2* __restrict__ scratch) {
+    __shared__ SelShared s;
+    const uint32_t k = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+    if (!is_fv_row(a.rows[b], a.V)) return;
+    FvRowState* st = fv_state_of(a, b);
+    if (st->active == 0u) return;
+    const RowCtx c = make_ctx(a.V, a.logits + (size_t)b * a.V, st->m, st->fmin, st->T, scratch + (size_t)b * a.V);
+    const FvPlan P = st->plan;
+    uint32_t beg, end;
+    fv_slice(a.V, kFvSlices, k, &beg, &end);
+    fv_gather(s, c, P, beg, end);
+    const uint32_t nl = s.bu[2];
+    __syncthreads();
+    if (tid == 0) {
+        if (nl > kCandCap) {
+            atomicOr(&st->overflow, 1u);
+            s.bu[3] = 0xFFFFFFFFu;
+        } else {
+            s.bu[3] = atomicAdd(&st->ncand, nl);
+        }
+    }
+    __syncthreads();
+    const uint32_t off = s.bu[3];
+    if (off != 0xFFFFFFFFu)
+        for (uint32_t i = tid; i < nl; i += kSelThreads)
+            if (off + i < kCandCap) a.fv_cand[(size_t)b * kCandCap + off + i] = s.cand[i];
+}
+
+// Sort of the gathered candidates and the draw, one workgroup per deferred row (the kernel
+// boundary orders it after every slice's stores).
+__global__ __launch_bounds__(kSelThreads) void k_fv_finish(SelectArgs a, uint2* __restrict__ scratch) {
+    __shared__ SelShared s;
+    const uint32_t b = blockIdx.x, tid = threadIdx.x;
+    if (!is_fv_row(a.rows[b], a.V)) return;
+    FvRowState* st = fv_state_of(a, b);
+    if (st->active == 0u) return;
+    const RowCtx c = make_ctx(a.V, a.logits + (size_t)b * a.V, st->m, st->fmin, st->T, scratch + (size_t)b * a.V);
+    const FvPlan P = st->plan;
+    const uint32_t n = st->ncand;
+    RowReport rep = {};
+    rep.max_logit = st->m;
+    rep.u = st->u;
+    rep.shortlist = st->want;
+    rep.total = st->Z;
+    uint32_t token = st->arg;
+    int ok = 0;
+    if (st->overflow == 0u && n > 0u && n <= kCandCap) {
+        for (uint32_t i = tid; i < n; i += kSelThreads) s.cand[i] = a.fv_cand[(size_t)b * kCandCap + i];
+        const unsigned long long* mg = a.fv_merged + (size_t)b * 2u * kVBins;
+        for (uint32_t i = tid; i < kVBins; i += kSelThreads) {
+            s.vm[i] = mg[i];
+            s.vq[i] = mg[kVBins + i];
+        }
+        __syncthreads();
+        double dn = 0.0, rr = 0.0;
+        uint32_t tk = 0;
+        ok = fv_finish(s, c, P, n, st->u, &tk, &dn, &rr);
+        if (ok) {
+            token = tk;
+            rep.denom = dn;
+            rep.r = rr;
+            rep.path = 2;
+        }
+    }
+    if (!ok) {
+        // too many candidates, or rounding outside the gathered bins: the one-workgroup paths
+        double dn = 0.0, rr = 0.0;
+        uint32_t tk = 0;
+        if (full_vocab_value_path(s, c, st->top_p, st->u, st->arg, &tk, &dn, &rr)) {
+            token = tk;
+            rep.denom = dn;
+            rep.r = rr;
+            rep.path = 2;
+        } else {
+            const DevRow row = a.rows[b];
+            radix_select(s, c, row, st->u, st->want, st->Z, st->arg, &token, &rep);
+        }
+    }
+    write_row(a, b, token, rep);
 }
 
 // ---- the kernel ----------------------------------------------------------------------------------
@@ -580,6 +846,8 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a, uint2* __r
     const float u = a.uniforms ? a.uniforms[b] : row.u;
     const BlockPartial* parts = a.partials + (size_t)b * a.ntile;
     const bool keys_cached = a.ntile <= kKeyCache;
+    // the multi-workgroup hand-over is re-armed below only for rows this step defers
+    if (a.fv_part && tid == 0 && is_fv_row(row, a.V)) fv_state_of(a, b)->active = 0u;
 
     // 0. the head epilogue has consumed this step's history counts: zero exactly the entries
     //    the step prep set (ids of the first clr_len entries; the append below writes past them)
@@ -656,6 +924,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a, uint2* __r
     rep.max_logit = m;
     rep.u = u;
     uint32_t token = arg;
+    bool deferred = false;  // finished by k_fv_finish
 
     if (row.temperature <= 0.0f) {
         rep.path = 0;
@@ -751,12 +1020,9 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a, uint2* __r
                     }
 #pragma unroll
                     for (int t = 0; t < 8; ++t) {
-                        if (id[t] >= a.V) continue;
                         const uint32_t k = float_key(v[t]);
-                        if (k >= tau) {
-                            const uint32_t slot = atomicAdd(&s.bu[4], 1u);
-                            if (slot < kCandCap) s.cand[slot] = ((unsigned long long)(~k) << 32) | id[t];
-                        }
+                        wave_append(&s.bu[4], id[t] < a.V && k >= tau, ((unsigned long long)(~k) << 32) | id[t],
+                                    s.cand, kCandCap);
                     }
                 }
                 __syncthreads();
@@ -853,17 +1119,52 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a, uint2* __r
             }
         }
         if (general) {
-            RowCtx c;
-            c.V = a.V;
-            c.l = lrow;
-            c.m = m;
-            c.T = row.temperature;
-            c.list = scratch + (size_t)b * a.V;
-            const float span = 48.0f * fmaxf(1.0f, row.temperature);
-            const float lo = fmaxf(fmin, m - span);
-            c.inv_w = (m > lo) ? (float)kVBins / (m - lo) : 0.0f;
+            const RowCtx c = make_ctx(a.V, lrow, m, fmin, row.temperature, scratch + (size_t)b * a.V);
             bool done = false;
-            if (want >= a.V) {
+            if (want >= a.V && a.fv_part) {
+                // multi-workgroup rows: merge the slice histograms (exact integer sums), plan,
+                // and leave the gather and the draw to k_fv_gather and k_fv_finish
+                const unsigned long long* part = a.fv_part + (size_t)b * kFvSlices * 2u * kVBins;
+                unsigned long long* mg = a.fv_merged + (size_t)b * 2u * kVBins;
+                for (uint32_t i = tid; i < kVBins; i += kSelThreads) {
+                    unsigned long long hm = 0ull, hq = 0ull;
+                    for (uint32_t k = 0; k < kFvSlices; ++k) {
+                        hm += part[(size_t)k * 2u * kVBins + i];
+                        hq += part[(size_t)k * 2u * kVBins + kVBins + i];
+                    }
+                    s.vm[i] = hm;
+                    s.vq[i] = hq;
+                    mg[i] = hm;
+                    mg[kVBins + i] = hq;
+                }
+                __syncthreads();
+                FvPlan P;
+                fv_plan(s, c, row.top_p, u, &P);
+                FvRowState* st = fv_state_of(a, b);
+                if (P.u_zero) {
+                    token = arg;
+                    rep.denom = P.A;
+                    rep.r = 0.0;
+                    rep.path = 2;
+                } else {
+                    deferred = true;
+                }
+                if (tid == 0) {
+                    st->plan = P;
+                    st->m = m;
+                    st->fmin = fmin;
+                    st->T = row.temperature;
+                    st->u = u;
+                    st->top_p = row.top_p;
+                    st->arg = arg;
+                    st->want = want;
+                    st->Z = Z;
+                    st->ncand = 0u;
+                    st->overflow = 0u;
+                    st->active = deferred ? 1u : 0u;
+                }
+                done = true;
+            } else if (want >= a.V) {
                 double dn = 0.0, rr = 0.0;
                 uint32_t tk = 0;
                 if (full_vocab_value_path(s, c, row.top_p, u, arg, &tk, &dn, &rr)) {
@@ -874,47 +1175,33 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a, uint2* __r
                     done = true;
                 }
             }
-            if (!done) {
-                // radix fallback: shortlist bound, nucleus, then the draw
-                uint32_t kx, ix;
-                PSet s0 = {0, 0u, 0u};
-                if (want < a.V && find_cross(s, c, s0, 0, (double)want, &kx, &ix)) s0 = PSet{1, kx, ix};
-                PSet s1 = s0;
-                if (row.top_p < 1.0f && find_cross(s, c, s0, 1, (double)row.top_p * Z, &kx, &ix))
-                    s1 = PSet{1, kx, ix};
-                double dl = 0.0;
-                row_pass(lrow, a.V, [&](float v, uint32_t i) {
-                    if (s1.has(float_key(v), i)) dl += (double)weight_f(c, v, 2);
-                });
-                const double tot = block_sum<double>(dl, s);
-                const double r = (double)u * tot;
-                if (!(r > 0.0)) token = arg;
-                else if (find_cross(s, c, s1, 2, r, &kx, &ix)) token = ix;
-                else token = s1.bounded ? s1.ib : arg;
-                rep.denom = tot;
-                rep.r = r;
-                rep.path = 4;
-            }
+            if (!done) radix_select(s, c, row, u, want, Z, arg, &token, &rep);
         }
     }
 
-    if (tid == 0) {
-        a.tokens[b] = token;
-        if (a.report) reinterpret_cast<RowReport*>(a.report)[b] = rep;
-        if (a.history && a.hist_len && token != 0xFFFFFFFFu) {
-            const uint32_t len = a.hist_len[b];
-            if (len < a.hist_stride) {
-                a.history[(size_t)b * a.hist_stride + len] = token;
-                a.hist_len[b] = len + 1u;
-            }
-        }
-    }
+    if (!deferred) write_row(a, b, token, rep);
 }
 
-void launch_select(const Head& h, int batch, const SelectArgs& a, hipStream_t st) {
-    hipLaunchKernelGGL(k_select, dim3((unsigned)batch), dim3(kSelThreads), 0, st, a,
-                       reinterpret_cast<uint2*>(h.list_scratch));
+void launch_select(const Head& h, int batch, const SelectArgs& args, bool any_fv, hipStream_t st) {
+    SelectArgs a = args;
+    const bool multi = any_fv && (uint32_t)batch <= kFvMaxBatch && h.fv_part;
+    a.fv_part = multi ? h.fv_part : nullptr;
+    a.fv_merged = h.fv_merged;
+    a.fv_cand = h.fv_cand;
+    a.fv_state = h.fv_state;
+    uint2* scratch = reinterpret_cast<uint2*>(h.list_scratch);
+    if (multi) {
+        hipLaunchKernelGGL(k_fv_hist, dim3(kFvSlices, (unsigned)batch), dim3(kSelThreads), 0, st, a);
+        check_hip(hipGetLastError(), "select (slice histograms)");
+    }
+    hipLaunchKernelGGL(k_select, dim3((unsigned)batch), dim3(kSelThreads), 0, st, a, scratch);
     check_hip(hipGetLastError(), "select");
+    if (multi) {
+        hipLaunchKernelGGL(k_fv_gather, dim3(kFvSlices, (unsigned)batch), dim3(kSelThreads), 0, st, a, scratch);
+        check_hip(hipGetLastError(), "select (slice gather)");
+        hipLaunchKernelGGL(k_fv_finish, dim3((unsigned)batch), dim3(kSelThreads), 0, st, a, scratch);
+        check_hip(hipGetLastError(), "select (finish)");
+    }
 }
 
 }  // namespace tdt
