@@ -454,50 +454,6 @@ __device__ inline int scan_cross(SelShared& s, const unsigned long long* h, uint
     return 1;
 }
 
-// Within the sorted list s.cand, elements [lo, hi] (inclusive, at most kCandCap): the first
-// index whose cumulative weight (exp2((v - m) * kw)) reaches rem, or hi; *sum receives the
-// weight of [lo, hi]. Thread t owns elements lo + [kPer t, kPer t + kPer).
-constexpr uint32_t kPer = kCandCap / kSelThreads;
-
-__device__ uint32_t list_cross(SelShared& s, const RowCtx& c, uint32_t lo, uint32_t hi, float kw,
-                               double rem, double* sum) {
-    const uint32_t tid = threadIdx.x;
-    double wv[kPer];
-    double lsum = 0.0;
-#pragma unroll
-    for (uint32_t t = 0; t < kPer; ++t) {
-        const uint32_t e = lo + kPer * tid + t;
-        double w = 0.0;
-        if (e <= hi) {
-            const float v = key_float(~(uint32_t)(s.cand[e] >> 32));
-            if (v != -INFINITY) w = (double)__builtin_amdgcn_exp2f((v - c.m) * kw);
-        }
-        wv[t] = w;
-        lsum += w;
-    }
-    double tot;
-    double run = block_excl_scan<double>(lsum, s, &tot);
-    if (sum) *sum = tot;
-    uint32_t first = 0xFFFFFFFFu;
-#pragma unroll
-    for (uint32_t t = 0; t < kPer; ++t) {
-        run += wv[t];
-        const uint32_t e = lo + kPer * tid + t;
-        if (e <= hi && first == 0xFFFFFFFFu && run >= rem) first = e;
-    }
-    first = block_min_u(first, s);
-    return first == 0xFFFFFFFFu ? hi : first;
-}
-
-// Index of the first sorted list element (of n) whose value bin is >= bin.
-__device__ uint32_t list_bin_start(SelShared& s, const RowCtx& c, uint32_t n, uint32_t bin) {
-    uint32_t first = 0xFFFFFFFFu;
-    for (uint32_t e = threadIdx.x; e < n; e += kSelThreads)
-        if (vbin(c, key_float(~(uint32_t)(s.cand[e] >> 32))) >= bin) first = min(first, e);
-    first = block_min_u(first, s);
-    return first == 0xFFFFFFFFu ? n : first;
-}
-
 // ---- full-vocabulary nucleus over value bins ------------------------------------------------
 // Pieces shared by the one-workgroup path (full_vocab_value_path) and the multi-workgroup path
 // of small batches (k_fv_hist, k_select, k_fv_gather, k_fv_finish): histogram, plan, gather, finish.
@@ -577,45 +533,132 @@ __device__ __attribute__((always_inline)) inline void fv_gather(SelShared& s, co
     __syncthreads();
 }
 
+// Weighted crossing inside one value bin of the candidate list s.cand[0, n) (unsorted): among
+// the elements of `bin` with key <= key_limit, in ascending key order (logit descending, id
+// ascending), the first whose cumulative weight exp2((v - m) * kw) reaches `target`. A second
+// level of 2048 sub-bins over the bin's value range (u64 fixed-point weights) locates the
+// crossing; only that sub-bin's elements are then sorted and summed exactly. Returns 1 with the
+// element's key and the weight before it; 0 when the sub-bin holds more than 1024 elements.
+__device__ int fine_cross(SelShared& s, const RowCtx& c, uint32_t n, uint32_t bin, unsigned long long key_limit,
+                          float kw, double target, unsigned long long* key_out, double* before_out) {
+    const uint32_t tid = threadIdx.x;
+    unsigned long long* hf = reinterpret_cast<unsigned long long*>(s.pkey);   // 2048 sub-bins
+    unsigned long long* sub = reinterpret_cast<unsigned long long*>(s.tiles); // <= 1024 elements
+    constexpr uint32_t kSubCap = kTileCap / 2u;
+    auto sub_of = [&](float v) {
+        const float f = ((c.m - v) * c.inv_w - (float)bin) * (float)kVBins;
+        return (f <= 0.0f) ? 0u : (f < (float)(kVBins - 1)) ? (uint32_t)f : kVBins - 1u;
+    };
+    auto in_set = [&](unsigned long long k, float v) { return k <= key_limit && vbin(c, v) == bin; };
+    for (uint32_t i = tid; i < kVBins; i += kSelThreads) hf[i] = 0ull;
+    __syncthreads();
+    for (uint32_t e = tid; e < n; e += kSelThreads) {
+        const unsigned long long k = s.cand[e];
+        const float v = key_float(~(uint32_t)(k >> 32));
+        if (v == -INFINITY || !in_set(k, v)) continue;
+        atomicAdd(&hf[sub_of(v)], to_fx(__builtin_amdgcn_exp2f((v - c.m) * kw)));
+    }
+    __syncthreads();
+    uint32_t sb;
+    double above;
+    if (!scan_cross(s, hf, kVBins, target, &sb, &above)) {
+        // target beyond the set's total (rounding): the last non-empty sub-bin
+        uint32_t last = 0u;
+        for (uint32_t i = tid; i < kVBins; i += kSelThreads) if (hf[i]) last = max(last, i + 1u);
+        last = kVBins - block_min_u(kVBins - last, s);  // block max via min
+        if (last == 0u) return 0;
+        sb = last - 1u;
+        (void)scan_cross(s, hf, sb, INFINITY, &last, &above);
+    }
+    if (tid == 0) s.bu[5] = 0u;
+    __syncthreads();
+    for (uint32_t e0 = 0; e0 < n; e0 += kSelThreads) {
+        const uint32_t e = e0 + tid;
+        bool take = false;
+        unsigned long long k = 0ull;
+        if (e < n) {
+            k = s.cand[e];
+            const float v = key_float(~(uint32_t)(k >> 32));
+            take = v != -INFINITY && in_set(k, v) && sub_of(v) == sb;
+        }
+        wave_append(&s.bu[5], take, k, sub, kSubCap);
+    }
+    __syncthreads();
+    const uint32_t ns = s.bu[5];
+    __syncthreads();
+    if (ns == 0u || ns > kSubCap) return 0;
+    // rank sort of the sub-bin (distinct keys)
+    unsigned long long mine = 0ull;
+    uint32_t rank = 0u;
+    if (tid < ns) {
+        mine = sub[tid];
+        for (uint32_t j = 0; j < ns; ++j) rank += (sub[j] < mine) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (tid < ns) sub[rank] = mine;
+    __syncthreads();
+    // exact crossing inside the sorted sub-bin
+    double w = 0.0;
+    if (tid < ns) w = (double)__builtin_amdgcn_exp2f((key_float(~(uint32_t)(sub[tid] >> 32)) - c.m) * kw);
+    const double run = block_excl_scan<double>(w, s, nullptr);
+    const uint32_t first = block_min_u((tid < ns && above + run + w >= target) ? tid : 0xFFFFFFFFu, s);
+    const uint32_t pick = (first == 0xFFFFFFFFu) ? ns - 1u : first;
+    if (tid == pick) {
+        s.bd[3] = above + run;
+        s.bu[6] = (uint32_t)sub[tid];
+        s.bu[7] = (uint32_t)(sub[tid] >> 32);
+    }
+    __syncthreads();
+    *key_out = ((unsigned long long)s.bu[7] << 32) | s.bu[6];
+    *before_out = s.bd[3];
+    __syncthreads();
+    return 1;
+}
+
+// Sum of exp2((v - m) * kw) over the candidates of `bin` with key <= key_limit.
+__device__ double bin_weight(SelShared& s, const RowCtx& c, uint32_t n, uint32_t bin, unsigned long long key_limit, float kw) {
+    double acc = 0.0;
+    for (uint32_t e = threadIdx.x; e < n; e += kSelThreads) {
+        const unsigned long long k = s.cand[e];
+        const float v = key_float(~(uint32_t)(k >> 32));
+        if (v != -INFINITY && k <= key_limit && vbin(c, v) == bin)
+            acc += (double)__builtin_amdgcn_exp2f((v - c.m) * kw);
+    }
+    return block_sum<double>(acc, s);
+}
+
 // From the n gathered candidates in s.cand (unsorted) and the histograms in s.vm / s.vq: the
 // nucleus cut inside bin cb and the temperature draw. Returns 1 with *token, 0 when rounding
-// put the draw outside the gathered bins (the caller falls back to the radix path).
+// put the draw outside the gathered bins or a sub-bin is a massive tie (radix fallback).
 __device__ int fv_finish(SelShared& s, const RowCtx& c, const FvPlan& P, uint32_t n, float u,
                          uint32_t* token, double* denom_out, double* r_out) {
     const float kq = kLog2e / c.T;
     const unsigned long long* hq = same_weights(c) ? s.vm : s.vq;
     if (n > kCandCap || n == 0u) return 0;
-    sort_cand(s, n);
     const uint32_t cb = P.cb;
-    // nucleus cut inside bin cb (its elements are the list's last block)
+    // nucleus cut inside bin cb: the element where the T = 1 weight reaches the target
     double denom = P.A;
-    uint32_t cstart = n, ecut = n - 1u;
+    unsigned long long ecut = ~0ull;
     if (cb < kVBins) {
-        cstart = list_bin_start(s, c, n, cb);
-        if (cstart >= n) return 0;
-        ecut = list_cross(s, c, cstart, n - 1u, kLog2e, P.target_w - P.wabove, nullptr);
-        double qin;
-        (void)list_cross(s, c, cstart, ecut, kq, INFINITY, &qin);
-        denom = P.A + qin;
+        double bef;
+        if (!fine_cross(s, c, n, cb, ~0ull, kLog2e, P.target_w - P.wabove, &ecut, &bef)) return 0;
+        denom = P.A + bin_weight(s, c, n, cb, ecut, kq);
     }
     const double r = (double)u * denom;
     *denom_out = denom;
     *r_out = r;
-    uint32_t e;
+    unsigned long long kt = 0ull;
+    double bef;
     if (cb < kVBins && r > P.A) {
-        e = list_cross(s, c, cstart, ecut, kq, r - P.A, nullptr);
+        if (!fine_cross(s, c, n, cb, ecut, kq, r - P.A, &kt, &bef)) return 0;
     } else {
         uint32_t db;
         double dab;
         if (!scan_cross(s, hq, cb, r, &db, &dab)) return 0;
         if (db < P.dlo || db > P.dhi) return 0;  // outside the gathered range (rounding)
-        const uint32_t dstart = list_bin_start(s, c, n, db);
-        const uint32_t dend = list_bin_start(s, c, n, db + 1u);
-        if (dstart >= dend) return 0;
-        e = list_cross(s, c, dstart, dend - 1u, kq, r - dab, nullptr);
+        if (!fine_cross(s, c, n, db, ~0ull, kq, r - dab, &kt, &bef)) return 0;
     }
-    *token = (uint32_t)s.cand[e];
-    __syncthreads();
+    *token = (uint32_t)kt;
     return 1;
 }
 
