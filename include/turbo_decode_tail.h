@@ -224,9 +224,11 @@ TURBO_DT_API int turbo_sample_logits(void* handle, float* logits, const TurboSte
 
 /* ---- measurement ------------------------------------------------------------------------- */
 
-/* When enabled, HIP events bracket every launch of the head kernel (the int4 GEMV / MFMA
- * kernel) on the handle's stream. turbo_lmhead_head_kernel_time synchronises and returns the
- * summed milliseconds and launch count since the last reset. */
+/* When enabled, the head kernel (the int4 GEMV / MFMA kernel) is launched with HIP start and
+ * stop events on the handle's stream. enable = 1 times every launch; enable = N > 1 times every
+ * N-th launch (the events add a few microseconds of gap around the timed launch, so sampling
+ * keeps a loop's throughput representative). turbo_lmhead_head_kernel_time synchronises and
+ * returns the summed milliseconds and the number of timed launches since the last reset. */
 TURBO_DT_API int turbo_lmhead_enable_head_timing(void* handle, int enable);
 TURBO_DT_API int turbo_lmhead_head_kernel_time(void* handle, double* total_ms, int* launches,
                                                int reset);

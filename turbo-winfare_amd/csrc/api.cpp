@@ -270,7 +270,7 @@ tdt::EpiArgs epi_args(const Head& h, float* logits, bool softcap) {
 
 void launch_head(HandleBox& bx, int B, const tdt::EpiArgs& ep) {
     Head& h = bx.h;
-    const bool timed = h.timing;
+    const bool timed = h.timing && (h.t_launch++ % h.t_stride) == 0u;
     if (timed && h.t_count >= Head::kTimerSlots) {
         check_hip(hipStreamSynchronize(h.stream), "timer fold");
         for (int i = 0; i < h.t_count; ++i) {
@@ -713,7 +713,10 @@ TURBO_DT_API int turbo_lmhead_enable_head_timing(void* handle, int enable) {
             check_hip(hipEventCreate(&h.t_stop[i]), "timer events");
         }
     }
+    if (enable < 0) throw std::runtime_error("enable must be >= 0");
     h.timing = enable != 0;
+    h.t_stride = enable > 1 ? static_cast<uint32_t>(enable) : 1u;
+    h.t_launch = 0;
     return 1;
     API_CATCH(0)
 }

@@ -69,6 +69,8 @@ struct Head {
 
     // Head-kernel timing.
     bool timing = false;
+    uint32_t t_stride = 1;       // time every t_stride-th head launch
+    uint64_t t_launch = 0;       // head launches since timing was enabled
     static constexpr int kTimerSlots = 1024;
     hipEvent_t t_start[kTimerSlots] = {};
     hipEvent_t t_stop[kTimerSlots] = {};

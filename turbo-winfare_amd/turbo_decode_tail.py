@@ -296,8 +296,9 @@ class LMHead:
         out = TurboStepOutputs(_ptr(tokens), None, _ptr(report))
         _ok(self.lib.turbo_sample_logits(self.h, _ptr(logits), C.byref(inp), C.byref(out)))
 
-    def enable_head_timing(self, on: bool = True) -> None:
-        _ok(self.lib.turbo_lmhead_enable_head_timing(self.h, 1 if on else 0))
+    def enable_head_timing(self, on: bool = True, every: int = 1) -> None:
+        """Time every `every`-th head launch with HIP events (0 launches when off)."""
+        _ok(self.lib.turbo_lmhead_enable_head_timing(self.h, max(1, int(every)) if on else 0))
 
     def head_kernel_time(self, reset: bool = False) -> tuple[float, int]:
         ms, n = C.c_double(), C.c_int()
