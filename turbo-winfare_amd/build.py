@@ -39,9 +39,13 @@ def hipcc() -> str:
     return str(cand) if cand.exists() else "hipcc"
 
 
+# Per-source additions to FLAGS (later flags win).
+SOURCE_FLAGS: dict[str, list[str]] = {}
+
+
 def _compile(src: str) -> Path:
     out = OBJ / (Path(src).stem + ".o")
-    cmd = [hipcc(), *FLAGS, "-c", str(CSRC / src), "-o", str(out)]
+    cmd = [hipcc(), *FLAGS, *SOURCE_FLAGS.get(src, []), "-c", str(CSRC / src), "-o", str(out)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr}")

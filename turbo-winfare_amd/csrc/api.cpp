@@ -373,14 +373,6 @@ int run_rows(HandleBox& bx, const TurboStepInputs* in, const TurboStepOutputs* o
         sa.hist_stride = in->history_stride;
         sa.hist_len = in->history_len;
     }
-    if (has_hist) {
-        sa.clr_history = in->history;
-        sa.clr_stride = in->history_stride;
-        sa.clr_len = in->history_len;
-    }
-    sa.hcount = h.hcount;
-    sa.hbits = h.hbits;
-    sa.hbw = h.hbw;
     tdt::launch_select(h, B, sa, any_fv, h.stream);
     return 1;
 }

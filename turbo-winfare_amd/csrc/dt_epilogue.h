@@ -37,13 +37,16 @@ __device__ inline float apply_entry(float l, const ModEntry& m, const DevRow& ro
 }
 
 // The modifiers of one id of batch row b: its history count (dense array, read only where the
-// id's bit is set) and its summed bias (the row's bias entries of tile `tile`).
-__device__ inline ModEntry lookup_mods(uint32_t id, uint32_t b, uint32_t tile, const DevRow& row,
+// id's bit is set in the bitmap word hw) and its summed bias (the row's bias entries of tile
+// `tile`). The count is zeroed once read: exactly one wave reads each (row, id), so the array
+// is clean again for the next step without a separate pass.
+__device__ inline ModEntry lookup_mods(uint32_t id, uint32_t b, uint32_t tile, uint32_t hw, const DevRow& row,
                                        const EpiArgs& ep) {
     ModEntry m{id, 0u, 0.0f, 0u};
-    if ((row.has_mods & 1u) && ep.hcount) {
-        const uint32_t w = ep.hbits[(size_t)b * ep.hbw + (id >> 5)];
-        if ((w >> (id & 31u)) & 1u) m.count = ep.hcount[(size_t)b * ep.V + id];
+    if ((hw >> (id & 31u)) & 1u) {
+        uint32_t* cp = ep.hcount + (size_t)b * ep.V + id;
+        m.count = *cp;
+        if (m.count) *cp = 0u;  // stored after the load it depends on
     }
     if ((row.has_mods & 2u) && ep.block_start) {
         const uint32_t* bs = ep.block_start + (size_t)b * (ep.ntile + 1) + tile;
@@ -67,7 +70,14 @@ __device__ inline void epilogue_wave(float acc, uint32_t b, uint32_t tile, uint3
     if (ep.cap > 0.0f) l = ep.cap * tanhf(l / ep.cap);
     const DevRow& row = ep.rows[b];
     if (row.has_mods && valid) {
-        const ModEntry m = lookup_mods(id, b, tile, row, ep);
+        // history bitmap word of this id; lanes 0 and 32 zero the tile's two words once read
+        uint32_t hw = 0u;
+        if ((row.has_mods & 1u) && ep.hcount) {
+            uint32_t* wp = ep.hbits + (size_t)b * ep.hbw + (id >> 5);
+            hw = *wp;
+            if ((id & 31u) == 0u && hw != 0u) *wp = 0u;
+        }
+        const ModEntry m = lookup_mods(id, b, tile, hw, row, ep);
         if (m.count || m.has_bias) l = apply_entry(l, m, row, ep.rep_limit);
     }
     if (ep.ban && valid) {

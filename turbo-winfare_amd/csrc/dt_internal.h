@@ -88,8 +88,8 @@ struct EpiArgs {
     const ModEntry* mods;      // [B][mod_cap] bias tables (rows with has_mods & 2)
     uint32_t mod_cap;
     const uint32_t* block_start;  // [B][ntile + 1] first bias entry per tile
-    const uint32_t* hcount;    // [B][V] history counts (rows with has_mods & 1)
-    const uint32_t* hbits;     // [B][hbw]
+    uint32_t* hcount;          // [B][V] history counts (rows with has_mods & 1); zeroed once read
+    uint32_t* hbits;           // [B][hbw] bit per id with a nonzero count; zeroed once read
     uint32_t hbw;
     const uint32_t* ban;       // [B][ban_stride] or null
     uint32_t ban_stride;
@@ -163,13 +163,6 @@ struct SelectArgs {
     uint32_t* history;            // append target or null
     uint32_t hist_stride;
     uint32_t* hist_len;
-    // history whose counts the step set (rows with has_mods & 1): cleared here
-    const uint32_t* clr_history;
-    uint32_t clr_stride;
-    const uint32_t* clr_len;
-    uint32_t* hcount;
-    uint32_t* hbits;
-    uint32_t hbw;
     // multi-workgroup full-vocabulary path (null fv_part: one workgroup per row)
     unsigned long long* fv_part;    // [B][kFvSlices][2][kFvBins] slice histograms
     unsigned long long* fv_merged;  // [B][2][kFvBins] merged histograms

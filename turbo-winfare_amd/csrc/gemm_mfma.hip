@@ -250,11 +250,14 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
         if (col_ok && ep.rows[bq].has_mods) {
             const DevRow row = ep.rows[bq];
             // history counts: the two bitmap words of this tile decide which ids to look up
+            // (both halves of the column read them; the low half zeroes them for the next step)
             uint32_t hb[2] = {0u, 0u};
             if ((row.has_mods & 1u) && ep.hcount) {
-                const uint32_t* hw = ep.hbits + (size_t)bq * ep.hbw + (base >> 5);
+                uint32_t* hw = ep.hbits + (size_t)bq * ep.hbw + (base >> 5);
                 hb[0] = hw[0];
                 if (base + 32u < ep.V) hb[1] = hw[1];
+                if (hl == 0u && hb[0] != 0u) hw[0] = 0u;
+                if (hl == 0u && hb[1] != 0u) hw[1] = 0u;
             }
             uint32_t s = 0, e = 0;
             const ModEntry* me = ep.mods + (size_t)bq * ep.mod_cap;
@@ -271,7 +274,11 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
                         const uint32_t rr = 32u * mb + acc_row(r, hl);
                         const uint32_t id = base + rr;
                         ModEntry m{id, 0u, 0.0f, 0u};
-                        if ((hb[mb] >> (rr & 31u)) & 1u) m.count = ep.hcount[(size_t)bq * ep.V + id];
+                        if ((hb[mb] >> (rr & 31u)) & 1u) {
+                            uint32_t* cp = ep.hcount + (size_t)bq * ep.V + id;
+                            m.count = *cp;
+                            if (m.count) *cp = 0u;  // read once per step; zeroed for the next
+                        }
                         for (uint32_t k = s; k < e; ++k) {
                             const ModEntry t = me[k];
                             if (t.id == id) { m.bias = t.bias; m.has_bias = 1u; }
@@ -310,7 +317,7 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
                 if (z > bmax) { bmax = z; barg = base + 32u * mb + acc_row(r, hl); }  // rows in increasing order
                 if (z != -INFINITY) bmin = fminf(bmin, z);
             }
-        bmin = fminf(bmin, __shfl_xor(bmin, 32, 64));
+        bmin = fminf(bmin, xor32(bmin));
         if (col_ok && ep.logits) {
             float* lrow = ep.logits + (size_t)bq * ep.V + base;
 #pragma unroll
@@ -329,8 +336,8 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
                     }
                 }
         }
-        const float om = __shfl_xor(bmax, 32, 64);
-        const uint32_t oa = (uint32_t)__shfl_xor((int)barg, 32, 64);
+        const float om = xor32(bmax);
+        const uint32_t oa = xor32(barg);
         if (om > bmax || (om == bmax && oa < barg)) { bmax = om; barg = oa; }
         float se = 0.0f;
         if (bmax != -INFINITY) {
@@ -341,7 +348,7 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
                 for (int r = 0; r < 16; ++r)
                     se += __builtin_amdgcn_exp2f(fmaf(acc[mb][nb][r], 1.4426950408889634f, -mb2));
         }
-        se += __shfl_xor(se, 32, 64);
+        se += xor32(se);
         if (col_ok && hl == 0u) {
             BlockPartial bp;
             bp.max = bmax;

@@ -81,8 +81,8 @@ void launch_repack(const Head& h, const uint8_t* W, const uint16_t* S, const uin
 // halves, with odd elements divided by 16 because their weight halves carry a factor 16.
 //
 // History counts: every history occurrence with id < V adds one to hcount[b][id] and sets the
-// id's bit in hbits[b] (global atomics); the select kernel clears both after the head epilogue
-// has read them, so they are zero between steps.
+// id's bit in hbits[b] (global atomics); the head epilogue zeroes both as it reads them, so
+// they are zero between steps.
 // Bias table: the bias entries are sorted by (id, list position) with a bitonic sort in LDS;
 // each run of equal ids becomes one entry whose value is the run's biases summed in list order
 // from 0.0f. Entries are written sorted by id; block_start[t] = number of entries with
@@ -149,9 +149,10 @@ __device__ void prep_row(const PrepArgs& a, uint32_t b, float* sx) {
             float m = 0.0f;
 #pragma unroll
             for (int t = 0; t < 8; ++t) m = fmaxf(m, fabsf(xs[t]));
-            m = fmaxf(m, __shfl_xor(m, 1, 64));
-            m = fmaxf(m, __shfl_xor(m, 2, 64));
-            m = fmaxf(m, __shfl_xor(m, 4, 64));
+            // maximum and sum over the 8 lanes of the group: two quad swaps, then the half-row mirror
+            m = fmaxf(m, dpp_mov<dpp::kXor1>(m));
+            m = fmaxf(m, dpp_mov<dpp::kXor2>(m));
+            m = fmaxf(m, dpp_mov<dpp::kHalfMirror>(m));
             int e = 0;
             (void)frexpf(m, &e);  // m = f * 2^e, f in [0.5, 1); e = 0 for m = 0
             int X[8];
@@ -161,9 +162,9 @@ __device__ void prep_row(const PrepArgs& a, uint32_t b, float* sx) {
                 X[t] = (int)rintf(ldexpf(xs[t], 21 - e));
                 sX += X[t];
             }
-            sX += __shfl_xor(sX, 1, 64);
-            sX += __shfl_xor(sX, 2, 64);
-            sX += __shfl_xor(sX, 4, 64);
+            sX += dpp_mov<dpp::kXor1>(sX);
+            sX += dpp_mov<dpp::kXor2>(sX);
+            sX += dpp_mov<dpp::kHalfMirror>(sX);
             if (j8 == 0u) {
                 a.xws[(size_t)b * G + g] = ldexpf(1.0f, e - 21);
                 a.xsum[(size_t)b * G + g] = (float)sX * ldexpf(1.0f, e - 21);
@@ -238,12 +239,7 @@ __device__ void modtable_row(const PrepArgs& a, uint32_t b, unsigned long long* 
     uint32_t cnt = 0;
     for (uint32_t i = i0; i < i0 + per && i < P; ++i) cnt += starts_run(i) ? 1u : 0u;
     const uint32_t lane = tid & 63u, wave = tid >> 6;
-    uint32_t incl = cnt;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t v = (uint32_t)__shfl_up((int)incl, o, 64);
-        if ((int)lane >= o) incl += v;
-    }
+    const uint32_t incl = wave_incl_scan(cnt, lane);
     if (lane == 63u) s_scan[wave] = incl;
     __syncthreads();
     if (tid == 0u) {

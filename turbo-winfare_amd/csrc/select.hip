@@ -31,13 +31,21 @@
 
 namespace tdt {
 
-constexpr uint32_t kSelThreads = 1024;
-constexpr uint32_t kSelWaves = kSelThreads / 64;
+// Workgroups run 1024 threads (bandwidth-bound full-vocabulary passes) or 256 (small batches,
+// where the per-row work is latency-bound: one wave per SIMD issues each uniform instruction
+// every 4 cycles instead of sharing the SIMD with three others). Device code reads the size at
+// run time.
+constexpr uint32_t kMaxSelThreads = 1024;
+constexpr uint32_t kMaxSelWaves = kMaxSelThreads / 64;
+__device__ inline uint32_t sel_nt() { return (uint32_t)__builtin_amdgcn_workgroup_size_x(); }
+__device__ inline uint32_t sel_nw() { return sel_nt() >> 6; }
 constexpr uint32_t kCandCap = 8192;
 constexpr uint32_t kTileCap = 2048;
 constexpr uint32_t kBins = 2048;
 constexpr uint32_t kVBins = 2048;
 constexpr uint32_t kKeyCache = 8192;  // block-maximum keys kept in LDS (ntile <= 8192)
+constexpr uint32_t kRegTiles = 4096;    // block partials held in registers (kRegTiles / threads each)
+constexpr uint32_t kGatherChunk = 16384;  // shortlist gather: elements loaded per workgroup round
 constexpr int kInflight = 4;          // float4 loads in flight per thread in row passes
 constexpr double kFx = 1099511627776.0;  // 2^40: fixed-point scale of histogram weights
 
@@ -66,28 +74,20 @@ struct SelShared {
     __attribute__((aligned(16))) unsigned long long cand[kCandCap];
     uint32_t tiles[kTileCap];
     uint32_t pkey[kKeyCache];
-    double wsum_d[kSelWaves];
-    uint32_t wsum_u[kSelWaves];
-    float wmax[kSelWaves];
-    uint32_t warg[kSelWaves];
-    float wmin[kSelWaves];
-    float wzm[kSelWaves];
-    double wzs[kSelWaves];
+    double wsum_d[kMaxSelWaves];
+    uint32_t wsum_u[kMaxSelWaves];
+    float wmax[kMaxSelWaves];
+    uint32_t warg[kMaxSelWaves];
+    float wmin[kMaxSelWaves];
+    float wzm[kMaxSelWaves];
+    double wzs[kMaxSelWaves];
+    uint32_t gcnt[64];  // per 16-lane group (at most 64 groups)
+    uint32_t gtau[64];
     double bd[4];
     uint32_t bu[8];
 };
 
 // ---- block primitives ------------------------------------------------------------------------
-
-template <typename T>
-__device__ inline T wave_incl_scan(T v, uint32_t lane) {
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const T n = __shfl_up(v, o, 64);
-        if ((int)lane >= o) v += n;
-    }
-    return v;
-}
 
 template <typename T>
 __device__ inline T* wslot(SelShared& s);
@@ -106,7 +106,7 @@ __device__ __attribute__((always_inline)) inline T block_excl_scan(T v, SelShare
     if (lane == 63u) ws[wave] = incl;
     __syncthreads();
     T off = T(0), all = T(0);
-    for (uint32_t w = 0; w < kSelWaves; ++w) {
+    for (uint32_t w = 0; w < sel_nw(); ++w) {
         const T x = ws[w];
         if (w < wave) off += x;
         all += x;
@@ -130,7 +130,7 @@ __device__ inline uint32_t block_min_u(uint32_t v, SelShared& s) {
     if (lane == 0) s.wsum_u[wave] = v;
     __syncthreads();
     uint32_t r = 0xFFFFFFFFu;
-    for (uint32_t w = 0; w < kSelWaves; ++w) r = min(r, s.wsum_u[w]);
+    for (uint32_t w = 0; w < sel_nw(); ++w) r = min(r, s.wsum_u[w]);
     __syncthreads();
     return r;
 }
@@ -149,7 +149,7 @@ template <typename T>
 __device__ inline int hist_cross(SelShared& s, uint32_t nb, T target, uint32_t* bin, T* above,
                                  bool clamp = false) {
     const uint32_t tid = threadIdx.x;
-    const uint32_t per = nb / kSelThreads;
+    const uint32_t per = nb / sel_nt();
     T loc = T(0);
     for (uint32_t j = 0; j < per; ++j) loc += hist_at<T>(s, nb - 1u - (tid * per + j));
     T tot;
@@ -182,51 +182,67 @@ __device__ inline int hist_cross(SelShared& s, uint32_t nb, T target, uint32_t* 
     return 1;
 }
 
-// Sorts s.cand[0, n) ascending; keys are distinct (the low word is the id). Up to one key per
-// thread, each thread counts the keys below its own (wave-uniform LDS reads, which broadcast)
-// and stores its key at that rank; larger lists take the bitonic network.
+// Sorts s.cand[0, n) ascending with the bitonic network (n padded to a power of two).
 __device__ inline void sort_cand(SelShared& s, uint32_t n) {
     const uint32_t tid = threadIdx.x;
-    if (n <= kSelThreads) {
-        unsigned long long k = 0;
-        uint32_t r = 0;
-        if (tid < n) {
-            k = s.cand[tid];
-            uint32_t j = 0;
-            for (; j + 2u <= n; j += 2u) {
-                const ulonglong2 pr = *reinterpret_cast<const ulonglong2*>(&s.cand[j]);
-                r += (pr.x < k ? 1u : 0u) + (pr.y < k ? 1u : 0u);
-            }
-            if (j < n) r += (s.cand[j] < k) ? 1u : 0u;
-        }
-        __syncthreads();
-        if (tid < n) s.cand[r] = k;
-        __syncthreads();
-        return;
-    }
     uint32_t P = 2;
     while (P < n) P <<= 1;
-    for (uint32_t i = n + tid; i < P; i += kSelThreads) s.cand[i] = ~0ull;
+    for (uint32_t i = n + tid; i < P; i += sel_nt()) s.cand[i] = ~0ull;
     __syncthreads();
-    block_sort_u64<kSelThreads>(s.cand, P);
+    if (sel_nt() == kMaxSelThreads) block_sort_u64<kMaxSelThreads>(s.cand, P);
+    else block_sort_u64<256>(s.cand, P);
 }
 
 // Stream compaction with one LDS atomic per wave: the active lanes with pred get consecutive
 // slots (in lane order) of dst through *counter; slots past cap are counted but not stored.
-__device__ __attribute__((always_inline)) inline void wave_append(uint32_t* counter, bool pred, unsigned long long key,
-                                   unsigned long long* dst, uint32_t cap) {
+template <typename T>
+__device__ __attribute__((always_inline)) inline void wave_append(uint32_t* counter, bool pred, T key, T* dst,
+                                                                  uint32_t cap) {
     const unsigned long long mask = __ballot(pred);
     if (mask == 0ull) return;
     const uint32_t lane = threadIdx.x & 63u;
     const int leader = __ffsll((long long)mask) - 1;
     uint32_t base = 0u;
     if ((int)lane == leader) base = atomicAdd(counter, (uint32_t)__popcll(mask));
-    base = (uint32_t)__shfl((int)base, leader, 64);
+    base = lane_read(base, leader);
     if (pred) {
         const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
                                                         __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
         if (base + rank < cap) dst[base + rank] = key;
     }
+}
+
+// Sum of v over aligned groups of P consecutive lanes (P a power of two <= 64, wave-uniform);
+// every lane of a group receives the group's sum. All 64 lanes must be active.
+__device__ inline uint32_t group_sum(uint32_t v, uint32_t P) {
+    if (P >= 2u) v += dpp_mov<dpp::kXor1>(v);
+    if (P >= 4u) v += dpp_mov<dpp::kXor2>(v);
+    if (P >= 8u) v += dpp_mov<dpp::kHalfMirror>(v);
+    if (P >= 16u) v += dpp_mov<dpp::kRor8>(v);
+    if (P >= 32u) v += (uint32_t)__shfl_xor((int)v, 16, 64);
+    if (P >= 64u) v += xor32(v);
+    return v;
+}
+
+// Places the W smallest of the n (at most one per thread) distinct keys s.cand[0, n) in ascending order
+// at s.cand[0, W). Each key's rank is counted by a group of P threads (P as large as the block
+// allows), each over every P-th key, and summed across the group.
+__device__ void rank_top(SelShared& s, uint32_t n, uint32_t W) {
+    const uint32_t tid = threadIdx.x;
+    uint32_t lg = 0;
+    while (lg < 6u && (n << (lg + 1u)) <= sel_nt()) ++lg;
+    const uint32_t P = 1u << lg;
+    const uint32_t i = tid >> lg, part = tid & (P - 1u);
+    unsigned long long k = 0ull;
+    uint32_t r = 0u;
+    if (i < n) {
+        k = s.cand[i];
+        for (uint32_t j = part; j < n; j += P) r += (s.cand[j] < k) ? 1u : 0u;
+    }
+    r = group_sum(r, P);
+    __syncthreads();
+    if (i < n && part == 0u && r < W) s.cand[r] = k;
+    __syncthreads();
 }
 
 // Visits every (value, index) of a row with kInflight independent loads per thread in flight.
@@ -236,16 +252,16 @@ __device__ inline void row_pass(const float* l, uint32_t V, F&& f) {
     if ((V & 3u) == 0u && ((uintptr_t)l & 15u) == 0u) {
         const float4* l4 = reinterpret_cast<const float4*>(l);
         const uint32_t V4 = V >> 2;
-        for (uint32_t base = 0; base < V4; base += kInflight * kSelThreads) {
+        for (uint32_t base = 0; base < V4; base += kInflight * sel_nt()) {
             float4 q[kInflight];
 #pragma unroll
             for (int j = 0; j < kInflight; ++j) {
-                const uint32_t idx = base + (uint32_t)j * kSelThreads + tid;
+                const uint32_t idx = base + (uint32_t)j * sel_nt() + tid;
                 q[j] = (idx < V4) ? l4[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
             }
 #pragma unroll
             for (int j = 0; j < kInflight; ++j) {
-                const uint32_t idx = base + (uint32_t)j * kSelThreads + tid;
+                const uint32_t idx = base + (uint32_t)j * sel_nt() + tid;
                 if (idx < V4) {
                     f(q[j].x, 4u * idx);
                     f(q[j].y, 4u * idx + 1u);
@@ -255,16 +271,16 @@ __device__ inline void row_pass(const float* l, uint32_t V, F&& f) {
             }
         }
     } else {
-        for (uint32_t base = 0; base < V; base += 4u * kInflight * kSelThreads) {
+        for (uint32_t base = 0; base < V; base += 4u * kInflight * sel_nt()) {
             float q[4 * kInflight];
 #pragma unroll
             for (int j = 0; j < 4 * kInflight; ++j) {
-                const uint32_t idx = base + (uint32_t)j * kSelThreads + tid;
+                const uint32_t idx = base + (uint32_t)j * sel_nt() + tid;
                 q[j] = (idx < V) ? l[idx] : 0.0f;
             }
 #pragma unroll
             for (int j = 0; j < 4 * kInflight; ++j) {
-                const uint32_t idx = base + (uint32_t)j * kSelThreads + tid;
+                const uint32_t idx = base + (uint32_t)j * sel_nt() + tid;
                 if (idx < V) f(q[j], idx);
             }
         }
@@ -322,15 +338,15 @@ __device__ inline uint32_t select_tied_id(SelShared& s, const uint2* list, uint3
     for (int lv = 0; lv < 3; ++lv) {
         const uint32_t nb = (lv < 2) ? 2048u : 1024u;
         const uint32_t sh = (lv == 0) ? 21u : (lv == 1) ? 10u : 0u;
-        for (uint32_t i = tid; i < kBins; i += kSelThreads) s.hu[i] = 0u;
+        for (uint32_t i = tid; i < kBins; i += sel_nt()) s.hu[i] = 0u;
         __syncthreads();
-        for (uint32_t i = tid; i < n; i += kSelThreads) {
+        for (uint32_t i = tid; i < n; i += sel_nt()) {
             const uint2 e = list[i];
             if (e.x == kx && (e.y & mask) == prefix) atomicAdd(&s.hu[(e.y >> sh) & (nb - 1u)], 1u);
         }
         __syncthreads();
         // smallest ids first: mirror the bins for hist_cross, which scans from the top
-        for (uint32_t i = tid; i < nb / 2; i += kSelThreads) {
+        for (uint32_t i = tid; i < nb / 2; i += sel_nt()) {
             const uint32_t t = s.hu[i];
             s.hu[i] = s.hu[nb - 1u - i];
             s.hu[nb - 1u - i] = t;
@@ -351,7 +367,7 @@ __device__ inline uint32_t select_tied_id(SelShared& s, const uint2* list, uint3
 __device__ int find_cross(SelShared& s, const RowCtx& c, const PSet& ps, int mode, double target,
                           uint32_t* kx, uint32_t* ix) {
     const uint32_t tid = threadIdx.x;
-    for (uint32_t i = tid; i < kBins; i += kSelThreads) s.hd[i] = 0ull;
+    for (uint32_t i = tid; i < kBins; i += sel_nt()) s.hd[i] = 0ull;
     __syncthreads();
     row_pass(c.l, c.V, [&](float v, uint32_t i) {
         const uint32_t k = float_key(v);
@@ -379,9 +395,9 @@ __device__ int find_cross(SelShared& s, const RowCtx& c, const PSet& ps, int mod
     for (int lv = 0; lv < 2; ++lv) {
         const uint32_t nb = (lv == 0) ? 2048u : 1024u;
         const uint32_t sh = (lv == 0) ? 10u : 0u;
-        for (uint32_t i = tid; i < kBins; i += kSelThreads) s.hd[i] = 0ull;
+        for (uint32_t i = tid; i < kBins; i += sel_nt()) s.hd[i] = 0ull;
         __syncthreads();
-        for (uint32_t i = tid; i < n; i += kSelThreads) {
+        for (uint32_t i = tid; i < n; i += sel_nt()) {
             const uint2 e = c.list[i];
             if ((e.x & mask) != prefix) continue;
             const float w = weight_f(c, key_float(e.x), mode);
@@ -400,7 +416,7 @@ __device__ int find_cross(SelShared& s, const RowCtx& c, const PSet& ps, int mod
     // ties: equal keys have equal weight w; the crossing is the j-th smallest tied id with
     // (j + 1) * w >= rem
     uint32_t nt = 0;
-    for (uint32_t i = tid; i < n; i += kSelThreads) nt += (c.list[i].x == kk) ? 1u : 0u;
+    for (uint32_t i = tid; i < n; i += sel_nt()) nt += (c.list[i].x == kk) ? 1u : 0u;
     nt = block_sum<uint32_t>(nt, s);
     const double w = (double)weight_f(c, key_float(kk), mode);
     uint32_t j = 0;
@@ -422,7 +438,7 @@ __device__ int find_cross(SelShared& s, const RowCtx& c, const PSet& ps, int mod
 __device__ inline int scan_cross(SelShared& s, const unsigned long long* h, uint32_t limit, double target,
                                  uint32_t* bin, double* above) {
     const uint32_t tid = threadIdx.x;
-    const uint32_t per = kVBins / kSelThreads;
+    const uint32_t per = kVBins / sel_nt();
     double loc = 0.0;
     for (uint32_t j = 0; j < per; ++j) {
         const uint32_t bi = tid * per + j;
@@ -471,7 +487,7 @@ __device__ inline bool same_weights(const RowCtx& c) { return kLog2e / c.T == kL
 __device__ __attribute__((always_inline)) inline void fv_hist(SelShared& s, const RowCtx& c, uint32_t beg, uint32_t end) {
     const float kq = kLog2e / c.T;
     const bool same = same_weights(c);  // T = 1: one weighting serves nucleus and draw
-    for (uint32_t i = threadIdx.x; i < kVBins; i += kSelThreads) { s.vm[i] = 0ull; s.vq[i] = 0ull; }
+    for (uint32_t i = threadIdx.x; i < kVBins; i += sel_nt()) { s.vm[i] = 0ull; s.vq[i] = 0ull; }
     __syncthreads();
     row_pass(c.l + beg, end - beg, [&](float v, uint32_t) {
         if (v == -INFINITY) return;
@@ -550,9 +566,9 @@ __device__ int fine_cross(SelShared& s, const RowCtx& c, uint32_t n, uint32_t bi
         return (f <= 0.0f) ? 0u : (f < (float)(kVBins - 1)) ? (uint32_t)f : kVBins - 1u;
     };
     auto in_set = [&](unsigned long long k, float v) { return k <= key_limit && vbin(c, v) == bin; };
-    for (uint32_t i = tid; i < kVBins; i += kSelThreads) hf[i] = 0ull;
+    for (uint32_t i = tid; i < kVBins; i += sel_nt()) hf[i] = 0ull;
     __syncthreads();
-    for (uint32_t e = tid; e < n; e += kSelThreads) {
+    for (uint32_t e = tid; e < n; e += sel_nt()) {
         const unsigned long long k = s.cand[e];
         const float v = key_float(~(uint32_t)(k >> 32));
         if (v == -INFINITY || !in_set(k, v)) continue;
@@ -564,7 +580,7 @@ __device__ int fine_cross(SelShared& s, const RowCtx& c, uint32_t n, uint32_t bi
     if (!scan_cross(s, hf, kVBins, target, &sb, &above)) {
         // target beyond the set's total (rounding): the last non-empty sub-bin
         uint32_t last = 0u;
-        for (uint32_t i = tid; i < kVBins; i += kSelThreads) if (hf[i]) last = max(last, i + 1u);
+        for (uint32_t i = tid; i < kVBins; i += sel_nt()) if (hf[i]) last = max(last, i + 1u);
         last = kVBins - block_min_u(kVBins - last, s);  // block max via min
         if (last == 0u) return 0;
         sb = last - 1u;
@@ -572,7 +588,7 @@ __device__ int fine_cross(SelShared& s, const RowCtx& c, uint32_t n, uint32_t bi
     }
     if (tid == 0) s.bu[5] = 0u;
     __syncthreads();
-    for (uint32_t e0 = 0; e0 < n; e0 += kSelThreads) {
+    for (uint32_t e0 = 0; e0 < n; e0 += sel_nt()) {
         const uint32_t e = e0 + tid;
         bool take = false;
         unsigned long long k = 0ull;
@@ -618,7 +634,7 @@ __device__ int fine_cross(SelShared& s, const RowCtx& c, uint32_t n, uint32_t bi
 // Sum of exp2((v - m) * kw) over the candidates of `bin` with key <= key_limit.
 __device__ double bin_weight(SelShared& s, const RowCtx& c, uint32_t n, uint32_t bin, unsigned long long key_limit, float kw) {
     double acc = 0.0;
-    for (uint32_t e = threadIdx.x; e < n; e += kSelThreads) {
+    for (uint32_t e = threadIdx.x; e < n; e += sel_nt()) {
         const unsigned long long k = s.cand[e];
         const float v = key_float(~(uint32_t)(k >> 32));
         if (v != -INFINITY && k <= key_limit && vbin(c, v) == bin)
@@ -740,7 +756,7 @@ __device__ inline bool is_fv_row(const DevRow& row, uint32_t V) { return row.tem
 __device__ void partial_max_min(SelShared& s, const BlockPartial* parts, uint32_t ntile, float* m_out, float* fmin_out) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     float bm = -INFINITY, bmin = INFINITY;
-    for (uint32_t t = tid; t < ntile; t += kSelThreads) {
+    for (uint32_t t = tid; t < ntile; t += sel_nt()) {
         const BlockPartial p = parts[t];
         bm = fmaxf(bm, p.max);
         bmin = fminf(bmin, p.minf);
@@ -750,7 +766,7 @@ __device__ void partial_max_min(SelShared& s, const BlockPartial* parts, uint32_
     if (lane == 0) { s.wmax[wave] = bm; s.wmin[wave] = bmin; }
     __syncthreads();
     float m = s.wmax[0], fmin = s.wmin[0];
-    for (uint32_t w = 1; w < kSelWaves; ++w) { m = fmaxf(m, s.wmax[w]); fmin = fminf(fmin, s.wmin[w]); }
+    for (uint32_t w = 1; w < sel_nw(); ++w) { m = fmaxf(m, s.wmax[w]); fmin = fminf(fmin, s.wmin[w]); }
     __syncthreads();
     *m_out = m;
     *fmin_out = fmin;
@@ -778,7 +794,7 @@ __device__ inline FvRowState* fv_state_of(const SelectArgs& a, uint32_t b) {
 }
 
 // Slice histograms of the full-vocabulary rows: workgroup (k, b) bins slice k of row b.
-__global__ __launch_bounds__(kSelThreads) void k_fv_hist(SelectArgs a) {
+__global__ __launch_bounds__(kMaxSelThreads) void k_fv_hist(SelectArgs a) {
     __shared__ SelShared s;
     const uint32_t k = blockIdx.x, b = blockIdx.y;
     const DevRow row = a.rows[b];
@@ -791,14 +807,14 @@ __global__ __launch_bounds__(kSelThreads) void k_fv_hist(SelectArgs a) {
     fv_slice(a.V, kFvSlices, k, &beg, &end);
     fv_hist(s, c, beg, end);
     unsigned long long* dst = a.fv_part + ((size_t)b * kFvSlices + k) * 2u * kVBins;
-    for (uint32_t i = threadIdx.x; i < kVBins; i += kSelThreads) {
+    for (uint32_t i = threadIdx.x; i < kVBins; i += sel_nt()) {
         dst[i] = s.vm[i];
         dst[kVBins + i] = s.vq[i];
     }
 }
 
 // Gather of the planned bins, slice k of row b, into the row's global candidate list.
-__global__ __launch_bounds__(kSelThreads) void k_fv_gather(SelectArgs a, uint2* __restrict__ scratch) {
+__global__ __launch_bounds__(kMaxSelThreads) void k_fv_gather(SelectArgs a, uint2* __restrict__ scratch) {
     __shared__ SelShared s;
     const uint32_t k = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
     if (!is_fv_row(a.rows[b], a.V)) return;
@@ -822,13 +838,13 @@ __global__ __launch_bounds__(kSelThreads) void k_fv_gather(SelectArgs a, uint2* 
     __syncthreads();
     const uint32_t off = s.bu[3];
     if (off != 0xFFFFFFFFu)
-        for (uint32_t i = tid; i < nl; i += kSelThreads)
+        for (uint32_t i = tid; i < nl; i += sel_nt())
             if (off + i < kCandCap) a.fv_cand[(size_t)b * kCandCap + off + i] = s.cand[i];
 }
 
 // Sort of the gathered candidates and the draw, one workgroup per deferred row (the kernel
 // boundary orders it after every slice's stores).
-__global__ __launch_bounds__(kSelThreads) void k_fv_finish(SelectArgs a, uint2* __restrict__ scratch) {
+__global__ __launch_bounds__(kMaxSelThreads) void k_fv_finish(SelectArgs a, uint2* __restrict__ scratch) {
     __shared__ SelShared s;
     const uint32_t b = blockIdx.x, tid = threadIdx.x;
     if (!is_fv_row(a.rows[b], a.V)) return;
@@ -845,9 +861,9 @@ __global__ __launch_bounds__(kSelThreads) void k_fv_finish(SelectArgs a, uint2* 
     uint32_t token = st->arg;
     int ok = 0;
     if (st->overflow == 0u && n > 0u && n <= kCandCap) {
-        for (uint32_t i = tid; i < n; i += kSelThreads) s.cand[i] = a.fv_cand[(size_t)b * kCandCap + i];
+        for (uint32_t i = tid; i < n; i += sel_nt()) s.cand[i] = a.fv_cand[(size_t)b * kCandCap + i];
         const unsigned long long* mg = a.fv_merged + (size_t)b * 2u * kVBins;
-        for (uint32_t i = tid; i < kVBins; i += kSelThreads) {
+        for (uint32_t i = tid; i < kVBins; i += sel_nt()) {
             s.vm[i] = mg[i];
             s.vq[i] = mg[kVBins + i];
         }
@@ -879,9 +895,57 @@ __global__ __launch_bounds__(kSelThreads) void k_fv_finish(SelectArgs a, uint2* 
     write_row(a, b, token, rep);
 }
 
+// Shortlist threshold from the block-maximum keys held in registers (key[j]: tile tid + j NT,
+// 0 past ntile): a histogram of the block maxima over kWinBins value bins of width 1/32 below
+// the row maximum m. With the want-th largest block maximum in bin j (counted from m down),
+// every block counted up to bin j lies at or above m - (j + 1) w up to rounding far below one
+// bin, so m - (j + 2) w bounds the want-th largest block maximum, and with it the want-th
+// largest logit, from below. One wave scans the bins. Needs |m| <= 1024 (value rounding << w)
+// and the want-th maximum inside the window; returns 0 (not found) otherwise.
+constexpr uint32_t kWinBins = 256;
+constexpr float kWinWidth = 1.0f / 32.0f;
+template <uint32_t KP>
+__device__ __attribute__((always_inline)) inline uint32_t window_bound(SelShared& s, const uint32_t* key, float m,
+                                                                       uint32_t want) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    if (!(fabsf(m) <= 1024.0f)) return 0u;  // uniform
+    for (uint32_t i = tid; i < kWinBins; i += sel_nt()) s.hu[i] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (uint32_t j = 0; j < KP; ++j) {
+        const float v = key_float(key[j]);
+        if (key[j] != 0u && v >= m - (float)kWinBins * kWinWidth)
+            atomicAdd(&s.hu[min(kWinBins - 1u, (uint32_t)((m - v) * (1.0f / kWinWidth)))], 1u);
+    }
+    __syncthreads();
+    if (wave == 0u) {
+        const uint4 c = *reinterpret_cast<const uint4*>(&s.hu[4u * lane]);  // bins 4 lane .. 4 lane + 3
+        const uint32_t sum = c.x + c.y + c.z + c.w;
+        const uint32_t incl = wave_incl_scan(sum, lane);
+        const unsigned long long mk = __ballot(incl >= want);
+        uint32_t res = 0u;
+        if (mk != 0ull) {
+            const uint32_t L = (uint32_t)__ffsll((long long)mk) - 1u;
+            const uint32_t before = lane_read(incl - sum, (int)L);
+            const uint4 cl = *reinterpret_cast<const uint4*>(&s.hu[4u * L]);
+            uint32_t q = 3u;
+            if (before + cl.x >= want) q = 0u;
+            else if (before + cl.x + cl.y >= want) q = 1u;
+            else if (before + cl.x + cl.y + cl.z >= want) q = 2u;
+            const uint32_t jb = 4u * L + q;
+            res = float_key(m - (float)(jb + 2u) * kWinWidth);
+        }
+        if (lane == 0u) s.bu[6] = res;
+    }
+    __syncthreads();
+    return s.bu[6];
+}
+
 // ---- the kernel ----------------------------------------------------------------------------------
 
-__global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a, uint2* __restrict__ scratch) {
+template <uint32_t NT>
+__global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__ scratch) {
+    constexpr uint32_t KP = kRegTiles / NT;  // block partials per thread on the register path
     __shared__ SelShared s;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t b = blockIdx.x;
@@ -892,76 +956,95 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a, uint2* __r
     // the multi-workgroup hand-over is re-armed below only for rows this step defers
     if (a.fv_part && tid == 0 && is_fv_row(row, a.V)) fv_state_of(a, b)->active = 0u;
 
-    // 0. the head epilogue has consumed this step's history counts: zero exactly the entries
-    //    the step prep set (ids of the first clr_len entries; the append below writes past them)
-    if ((row.has_mods & 1u) && a.clr_history && a.hcount) {
-        const uint32_t nh = min(a.clr_len[b], a.clr_stride);
-        const uint32_t* hist = a.clr_history + (size_t)b * a.clr_stride;
-        for (uint32_t i = tid; i < nh; i += kSelThreads) {
-            const uint32_t id = hist[i];
-            if (id < a.V) {
-                a.hcount[(size_t)b * a.V + id] = 0u;
-                a.hbits[(size_t)b * a.hbw + (id >> 5)] = 0u;
-            }
-        }
-    }
-
-    // 1. row max, lowest argmax and finite minimum over the block partials; the block-maximum
-    //    keys are kept in LDS for the shortlist threshold. Sampled rows also accumulate
-    //    Z = sum_t sumexp_t * exp(max_t - m) online (running maximum zm, rescaled sum zs).
+    // 1. row max, lowest argmax, finite minimum and, for sampled rows,
+    //    Z = sum_t sumexp_t * exp(max_t - m) over the block partials
     const bool sampled = row.temperature > 0.0f;
-    float bm = -INFINITY, bmin = INFINITY, zm = -INFINITY;
-    uint32_t ba = 0xFFFFFFFFu;
-    double zs = 0.0;
-    for (uint32_t t0 = tid; t0 < a.ntile; t0 += 4u * kSelThreads) {
-        BlockPartial p[4];
+    const bool reg = a.ntile <= kRegTiles;
+    uint32_t key[KP];  // register path: block-maximum keys of tiles tid + j NT (0 past ntile)
+    float m, fmin;
+    uint32_t arg;
+    double Z = 0.0;
+    if (reg) {
+        BlockPartial p[KP];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t t = t0 + (uint32_t)j * kSelThreads;
-            if (t < a.ntile) p[j] = parts[t];
+        for (uint32_t j = 0; j < KP; ++j) {
+            const uint32_t t = tid + j * NT;
+            p[j] = (t < a.ntile) ? parts[t] : BlockPartial{-INFINITY, 0xFFFFFFFFu, 0.0f, INFINITY};
+            key[j] = (t < a.ntile) ? float_key(p[j].max) : 0u;
         }
+        float bm = -INFINITY, bmin = INFINITY;
+        uint32_t ba = 0xFFFFFFFFu;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t t = t0 + (uint32_t)j * kSelThreads;
-            if (t >= a.ntile) continue;
+        for (uint32_t j = 0; j < KP; ++j) {
             if (p[j].max > bm || (p[j].max == bm && p[j].arg < ba)) { bm = p[j].max; ba = p[j].arg; }
             bmin = fminf(bmin, p[j].minf);
-            if (keys_cached) s.pkey[t] = float_key(p[j].max);
-            if (sampled && p[j].max != -INFINITY) {
-                if (p[j].max > zm) {
-                    if (zm != -INFINITY) zs *= (double)__builtin_amdgcn_exp2f((zm - p[j].max) * kLog2e);
-                    zm = p[j].max;
+        }
+        wave_argmax(bm, ba);
+        bmin = wave_min(bmin);
+        if (lane == 0) { s.wmax[wave] = bm; s.warg[wave] = ba; s.wmin[wave] = bmin; }
+        __syncthreads();
+        // every wave combines the wave results, one per lane
+        m = -INFINITY;
+        arg = 0xFFFFFFFFu;
+        fmin = INFINITY;
+        if (lane < sel_nw()) { m = s.wmax[lane]; arg = s.warg[lane]; fmin = s.wmin[lane]; }
+        wave_argmax(m, arg);
+        fmin = wave_min(fmin);
+        if (sampled && m != -INFINITY) {
+            double z = 0.0;
+#pragma unroll
+            for (uint32_t j = 0; j < KP; ++j)
+                if (p[j].max != -INFINITY)
+                    z += (double)(__builtin_amdgcn_exp2f((p[j].max - m) * kLog2e) * p[j].sumexp);
+            z = wave_sum_d(z);
+            if (lane == 0) s.wzs[wave] = z;
+        }
+        __syncthreads();
+        if (sampled && m != -INFINITY) Z = wave_sum_d(lane < sel_nw() ? s.wzs[lane] : 0.0);
+    } else {
+        // any number of tiles: a loop over the partials with a running maximum for Z; the
+        // block-maximum keys are kept in LDS when they fit
+        float bm = -INFINITY, bmin = INFINITY, zm = -INFINITY;
+        uint32_t ba = 0xFFFFFFFFu;
+        double zs = 0.0;
+        for (uint32_t t = tid; t < a.ntile; t += sel_nt()) {
+            const BlockPartial p = parts[t];
+            if (p.max > bm || (p.max == bm && p.arg < ba)) { bm = p.max; ba = p.arg; }
+            bmin = fminf(bmin, p.minf);
+            if (keys_cached) s.pkey[t] = float_key(p.max);
+            if (sampled && p.max != -INFINITY) {
+                if (p.max > zm) {
+                    if (zm != -INFINITY) zs *= (double)__builtin_amdgcn_exp2f((zm - p.max) * kLog2e);
+                    zm = p.max;
                 }
-                zs += (double)(__builtin_amdgcn_exp2f((p[j].max - zm) * kLog2e) * p[j].sumexp);
+                zs += (double)(__builtin_amdgcn_exp2f((p.max - zm) * kLog2e) * p.sumexp);
             }
         }
+        wave_argmax(bm, ba);
+        bmin = wave_min(bmin);
+        if (sampled) {
+            const float wm = wave_max(zm);
+            zs = (zm == -INFINITY) ? 0.0 : zs * (double)__builtin_amdgcn_exp2f((zm - wm) * kLog2e);
+            zs = wave_sum_d(zs);
+            zm = wm;
+        }
+        if (lane == 0) {
+            s.wmax[wave] = bm; s.warg[wave] = ba; s.wmin[wave] = bmin;
+            s.wzm[wave] = zm; s.wzs[wave] = zs;
+        }
+        __syncthreads();
+        m = -INFINITY;
+        arg = 0xFFFFFFFFu;
+        fmin = INFINITY;
+        float wzm = -INFINITY;
+        double wzs = 0.0;
+        if (lane < sel_nw()) { m = s.wmax[lane]; arg = s.warg[lane]; fmin = s.wmin[lane]; wzm = s.wzm[lane]; wzs = s.wzs[lane]; }
+        wave_argmax(m, arg);
+        fmin = wave_min(fmin);
+        if (sampled && m != -INFINITY)
+            Z = wave_sum_d(wzm != -INFINITY ? wzs * (double)__builtin_amdgcn_exp2f((wzm - m) * kLog2e) : 0.0);
+        __syncthreads();
     }
-    wave_argmax(bm, ba);
-    bmin = wave_min(bmin);
-    if (sampled) {
-        const float wm = wave_max(zm);
-        zs = (zm == -INFINITY) ? 0.0 : zs * (double)__builtin_amdgcn_exp2f((zm - wm) * kLog2e);
-        zs = wave_sum_d(zs);
-        zm = wm;
-    }
-    if (lane == 0) {
-        s.wmax[wave] = bm; s.warg[wave] = ba; s.wmin[wave] = bmin;
-        s.wzm[wave] = zm; s.wzs[wave] = zs;
-    }
-    __syncthreads();
-    float m = s.wmax[0], fmin = s.wmin[0];
-    uint32_t arg = s.warg[0];
-    for (uint32_t w = 1; w < kSelWaves; ++w) {
-        const float v = s.wmax[w];
-        const uint32_t i = s.warg[w];
-        if (v > m || (v == m && i < arg)) { m = v; arg = i; }
-        fmin = fminf(fmin, s.wmin[w]);
-    }
-    double Z = 0.0;
-    if (sampled && m != -INFINITY)
-        for (uint32_t w = 0; w < kSelWaves; ++w)
-            if (s.wzm[w] != -INFINITY) Z += s.wzs[w] * (double)__builtin_amdgcn_exp2f((s.wzm[w] - m) * kLog2e);
-    __syncthreads();
 
     RowReport rep = {};
     rep.max_logit = m;
@@ -980,7 +1063,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a, uint2* __r
         const uint32_t want = row.want;
         rep.shortlist = want;
         bool general = (want > kMaxTopK);
-        auto pkey = [&](uint32_t t) { return keys_cached ? s.pkey[t] : float_key(parts[t].max); };
+        auto pkey = [&](uint32_t t) { return (keys_cached && !reg) ? s.pkey[t] : float_key(parts[t].max); };
         if (!(Z > 0.0) || m == -INFINITY) {
             token = 0xFFFFFFFFu;
             rep.path = 3;
@@ -988,21 +1071,20 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a, uint2* __r
         } else if (!general) {
             // ---- shortlist path ----
             // tau: a lower bound of the want-th largest block maximum, hence of the want-th
-            // largest logit. First try one histogram of the block maxima over value bins of
-            // width 1/64 below m: with the want-th maximum in bin j (bins counted from m down),
-            // every counted block lies above m - (j + 1) w up to rounding far below one bin, so
-            // m - (j + 2) w is a safe bound. It needs |m| <= 1024 (value rounding << w) and the
-            // want-th maximum within kTauSpan of m; otherwise the exact 22-bit key bound (two
-            // 11-bit histogram levels).
+            // largest logit. With the keys in registers, a 256-bin window of width 1/32 below m
+            // (window_bound); else, or when the want-th maximum lies outside that window, one
+            // histogram of the block maxima over 2048 bins of width 1/64 (the same bound over a
+            // 32-unit span), and failing that the exact 22-bit key bound (two 11-bit levels).
             uint32_t tau = 0u;
-            if (a.ntile > want) {
+            if (a.ntile > want && reg) tau = window_bound<KP>(s, key, m, want);
+            if (a.ntile > want && tau == 0u) {
                 constexpr float kTauSpan = 32.0f;
                 constexpr float kTauInv = (float)kBins / kTauSpan;
                 bool found = false;
                 if (fabsf(m) <= 1024.0f) {
-                    for (uint32_t i = tid; i < kBins; i += kSelThreads) s.hu[i] = 0u;
+                    for (uint32_t i = tid; i < kBins; i += sel_nt()) s.hu[i] = 0u;
                     __syncthreads();
-                    for (uint32_t t = tid; t < a.ntile; t += kSelThreads) {
+                    for (uint32_t t = tid; t < a.ntile; t += sel_nt()) {
                         const float v = key_float(pkey(t));
                         if (v >= m - kTauSpan) {
                             const uint32_t j = min(kBins - 1u, (uint32_t)((m - v) * kTauInv));
@@ -1021,9 +1103,9 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a, uint2* __r
                     uint32_t prefix = 0, mask = 0, rem = want;
                     for (int lv = 0; lv < 2; ++lv) {
                         const uint32_t sh = (lv == 0) ? 21u : 10u;
-                        for (uint32_t i = tid; i < kBins; i += kSelThreads) s.hu[i] = 0u;
+                        for (uint32_t i = tid; i < kBins; i += sel_nt()) s.hu[i] = 0u;
                         __syncthreads();
-                        for (uint32_t t = tid; t < a.ntile; t += kSelThreads) {
+                        for (uint32_t t = tid; t < a.ntile; t += sel_nt()) {
                             const uint32_t k = pkey(t);
                             if ((k & mask) == prefix) atomicAdd(&s.hu[(k >> sh) & (kBins - 1u)], 1u);
                         }
@@ -1037,43 +1119,71 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a, uint2* __r
                     tau = prefix;
                 }
             }
-            if (tid == 0) { s.bu[3] = 0u; s.bu[4] = 0u; }
-            __syncthreads();
-            for (uint32_t t = tid; t < a.ntile; t += kSelThreads) {
-                if (pkey(t) >= tau) {
-                    const uint32_t slot = atomicAdd(&s.bu[3], 1u);
-                    if (slot < kTileCap) s.tiles[slot] = t;
+            // tiles whose maximum reaches tau, compacted into s.tiles
+            uint32_t nq = 0u;
+            if (reg) {
+                uint32_t hm = 0u;
+#pragma unroll
+                for (uint32_t j = 0; j < KP; ++j)
+                    if (key[j] >= tau && key[j] != 0u) hm |= 1u << j;
+                uint32_t o = block_excl_scan<uint32_t>((uint32_t)__popc(hm), s, &nq);
+#pragma unroll
+                for (uint32_t j = 0; j < KP; ++j)
+                    if ((hm >> j) & 1u) {
+                        if (o < kTileCap) s.tiles[o] = tid + j * NT;
+                        ++o;
+                    }
+                __syncthreads();
+            } else {
+                if (tid == 0) s.bu[3] = 0u;
+                __syncthreads();
+                for (uint32_t t = tid; t < a.ntile; t += NT) {
+                    if (pkey(t) >= tau) {
+                        const uint32_t slot = atomicAdd(&s.bu[3], 1u);
+                        if (slot < kTileCap) s.tiles[slot] = t;
+                    }
                 }
+                __syncthreads();
+                nq = s.bu[3];
             }
-            __syncthreads();
-            const uint32_t nq = s.bu[3];
             if (nq > kTileCap) {
                 general = true;
             } else {
-                // gather elements >= tau from the qualifying blocks, 8 loads in flight per thread
+                // gather the elements >= tau of those tiles: GB loads in flight per thread, a hit
+                // mask, one block scan for the output offsets per round
+                constexpr uint32_t GB = kGatherChunk / NT;
                 const uint32_t items = nq * kTileRows;
-                for (uint32_t it0 = tid; it0 < items; it0 += 8u * kSelThreads) {
-                    float v[8];
-                    uint32_t id[8];
+                uint32_t n = 0u;
+                for (uint32_t c0 = 0; c0 < items; c0 += kGatherChunk) {
+                    float v[GB];
+                    uint32_t id[GB];
 #pragma unroll
-                    for (int t = 0; t < 8; ++t) {
-                        const uint32_t it = it0 + (uint32_t)t * kSelThreads;
-                        id[t] = (it < items) ? s.tiles[it >> 6] * kTileRows + (it & 63u) : 0xFFFFFFFFu;
-                        v[t] = (id[t] < a.V) ? lrow[id[t]] : -INFINITY;
+                    for (uint32_t q = 0; q < GB; ++q) {
+                        const uint32_t it = c0 + q * NT + tid;
+                        id[q] = (it < items) ? s.tiles[it >> 6] * kTileRows + (it & 63u) : 0xFFFFFFFFu;
+                        v[q] = (id[q] < a.V) ? lrow[id[q]] : -INFINITY;
                     }
+                    uint32_t hm = 0u;
 #pragma unroll
-                    for (int t = 0; t < 8; ++t) {
-                        const uint32_t k = float_key(v[t]);
-                        wave_append(&s.bu[4], id[t] < a.V && k >= tau, ((unsigned long long)(~k) << 32) | id[t],
-                                    s.cand, kCandCap);
-                    }
+                    for (uint32_t q = 0; q < GB; ++q)
+                        if (id[q] < a.V && float_key(v[q]) >= tau) hm |= 1u << q;
+                    uint32_t tot = 0u;
+                    uint32_t o = n + block_excl_scan<uint32_t>((uint32_t)__popc(hm), s, &tot);
+#pragma unroll
+                    for (uint32_t q = 0; q < GB; ++q)
+                        if ((hm >> q) & 1u) {
+                            if (o < kCandCap) s.cand[o] = ((unsigned long long)(~float_key(v[q])) << 32) | id[q];
+                            ++o;
+                        }
+                    n += tot;
                 }
                 __syncthreads();
-                const uint32_t n = s.bu[4];
                 if (n > kCandCap) general = true;
                 __syncthreads();
                 if (!general) {
-                    sort_cand(s, n);
+                    // counting ranks costs n^2 / threads compares per thread: the network beyond 256
+                    if (n <= 256u) rank_top(s, n, min(want, n));
+                    else sort_cand(s, n);
                     // Nucleus over full-distribution probabilities p = exp(l - m) / Z (:139-151),
                     // then the draw over q = exp((l - m) / T) (:153-168). Both are computed for
                     // every shortlist entry; inclusive prefix sums up to the cut are unaffected by
@@ -1104,11 +1214,11 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a, uint2* __r
                             }
                             if (row.top_k > 0 && ct > (uint32_t)row.top_k) ct = (uint32_t)row.top_k;
                             if (ct < 1u) ct = 1u;
-                            const double dn = __shfl(runq, (int)ct - 1, 64);
+                            const double dn = lane_read(runq, (int)ct - 1);
                             const double rr = (double)u * dn;
                             const unsigned long long mk2 = __ballot(lane < ct && runq >= rr);
                             const uint32_t rk = mk2 ? (uint32_t)(__ffsll((long long)mk2) - 1) : ct - 1u;
-                            const uint32_t tk = (uint32_t)__shfl((int)idi, (int)rk, 64);
+                            const uint32_t tk = lane_read(idi, (int)rk);
                             if (lane == 0u) {
                                 s.bu[5] = tk; s.bu[6] = ct; s.bu[7] = rk;
                                 s.bd[1] = dn; s.bd[2] = rr;
@@ -1169,7 +1279,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a, uint2* __r
                 // and leave the gather and the draw to k_fv_gather and k_fv_finish
                 const unsigned long long* part = a.fv_part + (size_t)b * kFvSlices * 2u * kVBins;
                 unsigned long long* mg = a.fv_merged + (size_t)b * 2u * kVBins;
-                for (uint32_t i = tid; i < kVBins; i += kSelThreads) {
+                for (uint32_t i = tid; i < kVBins; i += sel_nt()) {
                     unsigned long long hm = 0ull, hq = 0ull;
                     for (uint32_t k = 0; k < kFvSlices; ++k) {
                         hm += part[(size_t)k * 2u * kVBins + i];
@@ -1234,15 +1344,15 @@ void launch_select(const Head& h, int batch, const SelectArgs& args, bool any_fv
     a.fv_state = h.fv_state;
     uint2* scratch = reinterpret_cast<uint2*>(h.list_scratch);
     if (multi) {
-        hipLaunchKernelGGL(k_fv_hist, dim3(kFvSlices, (unsigned)batch), dim3(kSelThreads), 0, st, a);
+        hipLaunchKernelGGL(k_fv_hist, dim3(kFvSlices, (unsigned)batch), dim3(kMaxSelThreads), 0, st, a);
         check_hip(hipGetLastError(), "select (slice histograms)");
     }
-    hipLaunchKernelGGL(k_select, dim3((unsigned)batch), dim3(kSelThreads), 0, st, a, scratch);
+    hipLaunchKernelGGL(k_select<kMaxSelThreads>, dim3((unsigned)batch), dim3(kMaxSelThreads), 0, st, a, scratch);
     check_hip(hipGetLastError(), "select");
     if (multi) {
-        hipLaunchKernelGGL(k_fv_gather, dim3(kFvSlices, (unsigned)batch), dim3(kSelThreads), 0, st, a, scratch);
+        hipLaunchKernelGGL(k_fv_gather, dim3(kFvSlices, (unsigned)batch), dim3(kMaxSelThreads), 0, st, a, scratch);
         check_hip(hipGetLastError(), "select (slice gather)");
-        hipLaunchKernelGGL(k_fv_finish, dim3((unsigned)batch), dim3(kSelThreads), 0, st, a, scratch);
+        hipLaunchKernelGGL(k_fv_finish, dim3((unsigned)batch), dim3(kMaxSelThreads), 0, st, a, scratch);
         check_hip(hipGetLastError(), "select (finish)");
     }
 }
