@@ -334,3 +334,33 @@ def test_full_vocab_rows_split_over_workgroups(head):
         check_sampler_on_gpu_logits([rows[b] for b in live], toks[live], base[live], [us[b] for b in live])
         paths = rep.view(np.uint32)[:, 5]
         assert all(paths[b] == 2 for b in live), paths
+
+
+@pytest.mark.parametrize("batch", [3, 12])
+def test_back_to_back_steps_match_synchronised(head, batch):
+    """Row parameters reach the kernels through the kernel arguments (batches up to 8) or a
+    pinned ring whose slots are refilled group by group. Many steps enqueued back to back, each
+    with its own temperature, top-k and uniform, must give exactly the tokens of the same steps
+    run one at a time with a synchronisation after each (where no slot can be reused early)."""
+    h, _ = head
+    steps = 40
+    x = dev(synth.hidden_states(batch, D, SEED + 5))
+    tok_all = torch.zeros((steps, batch), dtype=torch.int32, device="cuda")
+
+    def rows_for(s):
+        return [T.row_default(temperature=0.4 + 0.05 * ((s + b) % 9), top_k=[0, 1, 5, 40][(s + b) % 4] or 64,
+                              top_p=0.9, seed=77 + b, counter=s) for b in range(batch)]
+
+    keep = []
+    for s in range(steps):  # back to back
+        inp, k = h.make_inputs(batch, rows_for(s), hidden=x)
+        keep.append(k)
+        h.step(inp, tok_all[s])
+    h.sync()
+    async_toks = tok_all.cpu().numpy()
+    for s in range(steps):  # one at a time
+        inp, k = h.make_inputs(batch, rows_for(s), hidden=x)
+        t = torch.zeros(batch, dtype=torch.int32, device="cuda")
+        h.step(inp, t)
+        h.sync()
+        assert np.array_equal(t.cpu().numpy(), async_toks[s]), s

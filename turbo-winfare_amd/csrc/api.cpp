@@ -160,7 +160,7 @@ void free_head(Head& h) {
     dfree(h.fv_cand);
     dfree(h.fv_state);
     if (h.ring_host) (void)hipHostFree(h.ring_host);
-    for (int i = 0; i < Head::kRing; ++i)
+    for (int i = 0; i < Head::kRing / Head::kRingGroup; ++i)
         if (h.ring_ev[i]) (void)hipEventDestroy(h.ring_ev[i]);
     for (int i = 0; i < Head::kTimerSlots; ++i) {
         if (h.t_start[i]) (void)hipEventDestroy(h.t_start[i]);
@@ -168,27 +168,36 @@ void free_head(Head& h) {
     }
 }
 
-// Stages B DevRows in the next slot of the pinned ring and returns the slot's device-visible
-// address. The step-prep kernel copies the slot into device memory, so no separate copy is
-// enqueued; the slot is reused only after the event recorded behind that kernel has passed.
-const tdt::DevRow* stage_rows(Head& h, const tdt::DevRow* rows, int B, int* pos_out) {
+// Hands B DevRows to the step-prep kernel, which copies them into device memory (no separate
+// copy is enqueued). Up to kInlineRows ride in the kernel arguments. Larger batches use the next
+// slot of the pinned ring; a group of slots is refilled only after the event recorded behind the
+// prep kernel that read the group's last slot has passed. An event record costs the stream a
+// few microseconds (the queue drains and caches are written back for the host), so it is taken
+// once per group, not per step. Returns the ring slot used, -1 for none.
+int stage_rows(Head& h, const tdt::DevRow* rows, int B, tdt::PrepArgs* a) {
+    if (B <= tdt::kInlineRows) {
+        std::memcpy(a->inl, rows, sizeof(tdt::DevRow) * B);
+        a->rows_src = nullptr;
+        return -1;
+    }
     const int pos = h.ring_pos;
     h.ring_pos = (h.ring_pos + 1) % Head::kRing;
-    check_hip(hipEventSynchronize(h.ring_ev[pos]), "row staging wait");
+    if (pos % Head::kRingGroup == 0)
+        check_hip(hipEventSynchronize(h.ring_ev[pos / Head::kRingGroup]), "row staging wait");
     tdt::DevRow* slot = h.ring_host + static_cast<size_t>(pos) * h.max_batch;
     std::memcpy(slot, rows, sizeof(tdt::DevRow) * B);
-    *pos_out = pos;
-    return h.ring_dev + static_cast<size_t>(pos) * h.max_batch;
+    a->rows_src = h.ring_dev + static_cast<size_t>(pos) * h.max_batch;
+    return pos;
 }
 
 void release_slot(Head& h, int pos) {
-    check_hip(hipEventRecord(h.ring_ev[pos], h.stream), "row staging record");
+    if (pos >= 0 && pos % Head::kRingGroup == Head::kRingGroup - 1)
+        check_hip(hipEventRecord(h.ring_ev[pos / Head::kRingGroup], h.stream), "row staging record");
 }
 
-tdt::PrepArgs prep_args(const Head& h, const tdt::DevRow* src, int B) {
+tdt::PrepArgs prep_args(const Head& h, int B) {
     tdt::PrepArgs a{};
     a.B = B;
-    a.rows_src = src;
     a.rows_dst = h.rows;
     a.gamma = h.gamma;
     a.eps = h.eps;
@@ -213,9 +222,8 @@ tdt::PrepArgs prep_args(const Head& h, const tdt::DevRow* src, int B) {
 // Row parameters + (optionally) activations, no modifiers: one step-prep launch.
 void simple_prep(Head& h, const tdt::DevRow* rows, int B, const void* x, int dtype, bool normed,
                  float* xn, tdt::HeadPath path) {
-    int pos = 0;
-    const tdt::DevRow* src = stage_rows(h, rows, B, &pos);
-    tdt::PrepArgs a = prep_args(h, src, B);
+    tdt::PrepArgs a = prep_args(h, B);
+    const int pos = stage_rows(h, rows, B, &a);
     a.hidden = x;
     a.dtype = dtype;
     a.normed = normed ? 1 : 0;
@@ -331,9 +339,8 @@ int run_rows(HandleBox& bx, const TurboStepInputs* in, const TurboStepOutputs* o
     if (has_bias) P = tdt::modtable_sort_size(h, in->bias_stride);
     float* logits = given_logits ? given_logits : (out->logits ? out->logits : (all_greedy ? nullptr : h.logits));
 
-    int pos = 0;
-    const tdt::DevRow* src = stage_rows(h, rows, B, &pos);
-    tdt::PrepArgs pa = prep_args(h, src, B);
+    tdt::PrepArgs pa = prep_args(h, B);
+    const int pos = stage_rows(h, rows, B, &pa);
     pa.hidden = hidden;
     pa.dtype = in->hidden_dtype == TURBO_HIDDEN_BF16 ? 1 : 0;
     pa.normed = (in->flags & TURBO_STEP_NORMED) ? 1 : 0;
@@ -503,7 +510,7 @@ TURBO_DT_API void* turbo_lmhead_create(const TurboLMHeadDesc* d) {
                   "alloc pinned ring");
         check_hip(hipHostGetDevicePointer(reinterpret_cast<void**>(&h.ring_dev), h.ring_host, 0),
                   "map pinned ring");
-        for (int i = 0; i < Head::kRing; ++i)
+        for (int i = 0; i < Head::kRing / Head::kRingGroup; ++i)
             check_hip(hipEventCreateWithFlags(&h.ring_ev[i], hipEventDisableTiming), "ring events");
         check_hip(hipDeviceSynchronize(), "create");
     } catch (...) {

@@ -13,7 +13,7 @@ namespace tdt {
 // not limited: occurrences are counted in a dense per-row array.
 constexpr uint32_t kModCap = 8192;
 // Static LDS of the step-prep kernel, in u64 words: kModCap sort keys plus kModCap + 1 run
-// starts (u32); the RMSNorm blocks reuse it for the hidden row (D floats).
+// starts (u32).
 constexpr uint32_t kPrepPoolU64 = kModCap + (kModCap + 2u) / 2u;
 
 // Device-resident head plus per-step scratch. All sizes are fixed at create time.
@@ -61,10 +61,13 @@ struct Head {
     void* fv_state = nullptr;                 // [kFvMaxBatch] x kFvStateBytes
 
     // Host staging ring for DevRow uploads (pinned).
-    static constexpr int kRing = 8;
+    // Rows of batches above kInlineRows are staged in a ring of pinned slots, reused group by
+    // group: one event per kRingGroup steps marks the group's slots as read.
+    static constexpr int kRing = 16;
+    static constexpr int kRingGroup = 8;
     DevRow* ring_host = nullptr;       // [kRing][max_batch], pinned, mapped, coherent
     DevRow* ring_dev = nullptr;        // device-visible address of ring_host
-    hipEvent_t ring_ev[kRing] = {};
+    hipEvent_t ring_ev[kRing / kRingGroup] = {};
     int ring_pos = 0;
 
     // Head-kernel timing.
@@ -99,9 +102,12 @@ struct EpiArgs {
 enum class HeadPath { Digits, Mfma };
 
 // prep.hip
+// Batches of at most this many rows pass their parameters in the step-prep kernel arguments.
+constexpr int kInlineRows = 8;
 struct PrepArgs {
     int B;
-    const DevRow* rows_src;      // host-mapped staging slot (or device memory)
+    const DevRow* rows_src;      // host-mapped staging slot (null: the rows are in inl)
+    DevRow inl[kInlineRows];     // the rows of a small batch
     DevRow* rows_dst;            // device row buffer, filled by block 0 (null: no copy block)
     // activations (null hidden: no activation work)
     const void* hidden;

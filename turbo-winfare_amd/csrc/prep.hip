@@ -2,8 +2,8 @@
 //
 //  k_repack_w / k_repack_sb : reference layout -> tiled layout (once, at create)
 //  k_step_prep              : one block copies the staged per-row parameters to device memory;
-//                             one block per row runs the final RMSNorm
-//                             (src/cpu_reference.cpp:43-52) and writes the activation format the
+//                             ceil(D / 1024) blocks per row run the final RMSNorm
+//                             (src/cpu_reference.cpp:43-52) and write the activation format the
 //                             head kernel reads (digit planes for B <= 2, k-permuted fp16 for
 //                             B > 2); one block per row with modifiers counts the row's history
 //                             occurrences per id and builds its bias table sorted by id (summed
@@ -64,8 +64,8 @@ void launch_repack(const Head& h, const uint8_t* W, const uint16_t* S, const uin
 // ---- per-step preparation (one launch) -------------------------------------------------------
 // Row copy block: the per-row parameters from the host staging slot (pinned, mapped) into
 //   device memory for the later kernels.
-// RMSNorm blocks, one per batch row: final RMSNorm (src/cpu_reference.cpp:43-52) and the
-//   activation format the head kernel reads.
+// RMSNorm blocks, ceil(D / 1024) per batch row: final RMSNorm (src/cpu_reference.cpp:43-52)
+//   and the activation format the head kernel reads, 1024 elements per block.
 // Modifier blocks, one per batch row (only when some row uses modifiers): history counts and
 //   the bias table.
 //
@@ -74,7 +74,8 @@ void launch_repack(const Head& h, const uint8_t* W, const uint16_t* S, const uin
 // as six balanced base-16 digits d_k in [-8, 7] (X = sum d_k 16^k), packed eight per word in
 // element order, so v_dot8_i32_i4 consumes them against the weight nibbles directly. The
 // group's scale-back factor 2^(e-21) and sum(X) * 2^(e-21) are stored beside them. Eight lanes
-// share a group, each owning one packed word per digit.
+// A wave holds one group (lane = element); the eight lanes of an octet OR their nibbles into
+// one packed word per digit.
 //
 // fp16 (MFMA path): x rounded to fp16 and stored k-permuted within each octet as
 // (x0, x4, x1/16, x5/16, x2, x6, x3/16, x7/16): the order in which the weight dequant produces
@@ -89,107 +90,83 @@ void launch_repack(const Head& h, const uint8_t* W, const uint16_t* S, const uin
 // id < 64 t comes from a binary search over the run ids.
 constexpr uint32_t kPrepThreads = 1024;
 constexpr uint32_t kPrepWaves = kPrepThreads / 64;
-static_assert(kPrepPoolU64 * 8u >= 8192u * 4u, "the pool must hold the largest hidden row");
 
-__device__ void prep_row(const PrepArgs& a, uint32_t b, float* sx) {
+// RMSNorm block k of row b: every block sums the squares of the whole row (the row is small and
+// L2-resident; all blocks of a row compute the same sum in the same order), then normalises and
+// converts its own kPrepThreads elements, one per thread. A wave then holds exactly one 64-element
+// group, so the group's scale and digit words come from wave reductions.
+__device__ void prep_row(const PrepArgs& a, uint32_t b, uint32_t k) {
 #pragma clang fp contract(off)
     __shared__ double red[kPrepWaves];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t D = a.D;
-    // hidden and norm weight for this thread's elements, loaded together (one round trip)
+    const uint32_t i = k * kPrepThreads + tid;  // this thread's element
+    auto load = [&](uint32_t j) -> float {
+        if (a.dtype == 1) return bf16_to_f32(reinterpret_cast<const uint16_t*>(a.hidden)[(size_t)b * D + j]);
+        return reinterpret_cast<const float*>(a.hidden)[(size_t)b * D + j];
+    };
+    // the whole row for the sum (one round trip), this element's norm weight alongside
     constexpr uint32_t kPer = 8;  // D <= 8192 = kPer * kPrepThreads
-    float xv[kPer], gv[kPer];
+    float xv[kPer];
 #pragma unroll
-    for (uint32_t k = 0; k < kPer; ++k) {
-        const uint32_t i = tid + k * kPrepThreads;
-        float v = 0.0f, gw = 1.0f;
-        if (i < D) {
-            if (a.dtype == 1) v = bf16_to_f32(reinterpret_cast<const uint16_t*>(a.hidden)[(size_t)b * D + i]);
-            else v = reinterpret_cast<const float*>(a.hidden)[(size_t)b * D + i];
-            if (a.gamma) gw = bf16_to_f32(a.gamma[i]);
-        }
-        xv[k] = v;
-        gv[k] = gw;
+    for (uint32_t q = 0; q < kPer; ++q) {
+        const uint32_t j = tid + q * kPrepThreads;
+        xv[q] = (j < D) ? load(j) : 0.0f;
     }
+    const float gw = (a.gamma && i < D) ? bf16_to_f32(a.gamma[i]) : 1.0f;
+    float v = (k < kPer) ? xv[0] : 0.0f;
+#pragma unroll
+    for (uint32_t q = 1; q < kPer; ++q)
+        if (q == k) v = xv[q];
     if (!a.normed) {
         // src/cpu_reference.cpp:44-46: double sum of squares, float mean + eps, 1/sqrt.
         double acc = 0.0;
 #pragma unroll
-        for (uint32_t k = 0; k < kPer; ++k) acc += (double)xv[k] * (double)xv[k];
+        for (uint32_t q = 0; q < kPer; ++q) acc += (double)xv[q] * (double)xv[q];
         acc = wave_sum_d(acc);
         if (lane == 0) red[wave] = acc;
         __syncthreads();
-        double tot = 0.0;
-        for (uint32_t w = 0; w < kPrepWaves; ++w) tot += red[w];
+        const double tot = wave_sum_d(lane < kPrepWaves ? red[lane] : 0.0);
         const float ms = (float)(tot / (double)D);
         // sqrtf and 1.0f / s, each correctly rounded: computed in double and rounded once to
         // float, which is exact for sqrt and division (53 >= 2 * 24 + 2 bits).
         const float sq = (float)sqrt((double)(ms + a.eps));
         const float inv = (float)(1.0 / (double)sq);
-#pragma unroll
-        for (uint32_t k = 0; k < kPer; ++k) {
-            float v = xv[k] * inv;
-            if (a.gamma) v = v * gv[k];
-            xv[k] = v;
-        }
+        v = v * inv;
+        if (a.gamma) v = v * gw;
     }
-#pragma unroll
-    for (uint32_t k = 0; k < kPer; ++k) {
-        const uint32_t i = tid + k * kPrepThreads;
-        if (i < D) sx[i] = xv[k];
-    }
-    __syncthreads();
-    if (a.xn)
-        for (uint32_t i = tid; i < D; i += kPrepThreads) a.xn[(size_t)b * D + i] = sx[i];
+    if (i >= D) return;  // whole waves: D is a multiple of the 64-element group
+    if (a.xn) a.xn[(size_t)b * D + i] = v;
     if (a.path == 0) {
         const uint32_t G = D / kGroup, NC = D / 32u;
-        for (uint32_t q = tid; q < G * 8u; q += kPrepThreads) {  // 8 lanes per group
-            const uint32_t g = q >> 3, j8 = q & 7u;
-            const float* xs = sx + g * kGroup + 8u * j8;
-            float m = 0.0f;
+        const uint32_t g = i / kGroup;  // this wave's group
+        const float m = wave_max(fabsf(v));
+        int e = 0;
+        (void)frexpf(m, &e);  // m = f * 2^e, f in [0.5, 1); e = 0 for m = 0
+        int X = (int)rintf(ldexpf(v, 21 - e));
+        const int sX = wave_sum_i(X);
+        if (lane == 0u) {
+            a.xws[(size_t)b * G + g] = ldexpf(1.0f, e - 21);
+            a.xsum[(size_t)b * G + g] = (float)sX * ldexpf(1.0f, e - 21);
+        }
+        // six balanced base-16 digits; the eight lanes of an octet OR their nibbles into one word
+        const uint32_t j8 = lane >> 3, c = 2u * g + (j8 >> 2), wi = j8 & 3u;
+        uint32_t* dst = a.xdig + (((size_t)b * NC + c) * kDigits) * 4u + wi;
 #pragma unroll
-            for (int t = 0; t < 8; ++t) m = fmaxf(m, fabsf(xs[t]));
-            // maximum and sum over the 8 lanes of the group: two quad swaps, then the half-row mirror
-            m = fmaxf(m, dpp_mov<dpp::kXor1>(m));
-            m = fmaxf(m, dpp_mov<dpp::kXor2>(m));
-            m = fmaxf(m, dpp_mov<dpp::kHalfMirror>(m));
-            int e = 0;
-            (void)frexpf(m, &e);  // m = f * 2^e, f in [0.5, 1); e = 0 for m = 0
-            int X[8];
-            int sX = 0;
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                X[t] = (int)rintf(ldexpf(xs[t], 21 - e));
-                sX += X[t];
-            }
-            sX += dpp_mov<dpp::kXor1>(sX);
-            sX += dpp_mov<dpp::kXor2>(sX);
-            sX += dpp_mov<dpp::kHalfMirror>(sX);
-            if (j8 == 0u) {
-                a.xws[(size_t)b * G + g] = ldexpf(1.0f, e - 21);
-                a.xsum[(size_t)b * G + g] = (float)sX * ldexpf(1.0f, e - 21);
-            }
-            const uint32_t c = 2u * g + (j8 >> 2), wi = j8 & 3u;
-            uint32_t* dst = a.xdig + (((size_t)b * NC + c) * kDigits) * 4u + wi;
-#pragma unroll
-            for (uint32_t k = 0; k < kDigits; ++k) {
-                uint32_t word = 0u;
-#pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    const int d = ((X[t] + 8) & 15) - 8;
-                    X[t] = (X[t] - d) >> 4;
-                    word |= ((uint32_t)d & 15u) << (4 * t);
-                }
-                dst[k * 4u] = word;
-            }
+        for (uint32_t q = 0; q < kDigits; ++q) {
+            const int d = ((X + 8) & 15) - 8;
+            X = (X - d) >> 4;
+            uint32_t w = ((uint32_t)d & 15u) << (4u * (lane & 7u));
+            w |= dpp_mov<dpp::kXor1>(w);
+            w |= dpp_mov<dpp::kXor2>(w);
+            w |= dpp_mov<dpp::kHalfMirror>(w);
+            if ((lane & 7u) == 0u) dst[q * 4u] = w;
         }
     } else {
-        for (uint32_t i = tid; i < D; i += kPrepThreads) {
-            const uint32_t e = i & 7u;
-            const uint32_t slot = (e < 4u) ? 2u * e : 2u * (e - 4u) + 1u;
-            const _Float16 hv = (_Float16)((e & 1u) ? sx[i] * 0.0625f : sx[i]);
-            a.x16[(size_t)b * D + (i & ~7u) + slot] = __builtin_bit_cast(uint16_t, hv);
-        }
+        const uint32_t e = i & 7u;
+        const uint32_t slot = (e < 4u) ? 2u * e : 2u * (e - 4u) + 1u;
+        const _Float16 hv = (_Float16)((e & 1u) ? v * 0.0625f : v);
+        a.x16[(size_t)b * D + (i & ~7u) + slot] = __builtin_bit_cast(uint16_t, hv);
     }
 }
 
@@ -281,14 +258,17 @@ __device__ void modtable_row(const PrepArgs& a, uint32_t b, unsigned long long* 
     if (tid == 0u) a.mod_count[b] = nruns;
 }
 
-// Grid: [row copy block if rows_dst] [B RMSNorm blocks if hidden] [B table blocks if mods].
+// Grid: [row copy block if rows_dst] [B x ceil(D / 1024) RMSNorm blocks if hidden]
+// [B table blocks if mods].
 __global__ __launch_bounds__(kPrepThreads) void k_step_prep(PrepArgs a) {
     __shared__ unsigned long long pool[kPrepPoolU64];
     uint32_t blk = blockIdx.x;
     if (a.rows_dst) {
         if (blk == 0u) {
-            // A PCIe round trip: on a block of its own, so no other block waits for it.
-            const uint32_t* src = reinterpret_cast<const uint32_t*>(a.rows_src);
+            // From the kernel arguments, or a PCIe round trip to the pinned staging slot: on a
+            // block of its own, so no other block waits for it.
+            const uint32_t* src = a.rows_src ? reinterpret_cast<const uint32_t*>(a.rows_src)
+                                             : reinterpret_cast<const uint32_t*>(&a.inl[0]);
             uint32_t* dst = reinterpret_cast<uint32_t*>(a.rows_dst);
             for (uint32_t i = threadIdx.x; i < (uint32_t)a.B * (sizeof(DevRow) / 4); i += kPrepThreads)
                 dst[i] = src[i];
@@ -297,18 +277,20 @@ __global__ __launch_bounds__(kPrepThreads) void k_step_prep(PrepArgs a) {
         --blk;
     }
     if (a.hidden) {
-        if (blk < (uint32_t)a.B) {
-            prep_row(a, blk, reinterpret_cast<float*>(pool));
+        const uint32_t per = (a.D + kPrepThreads - 1u) / kPrepThreads;  // RMSNorm blocks per row
+        if (blk < (uint32_t)a.B * per) {
+            prep_row(a, blk / per, blk % per);
             return;
         }
-        blk -= (uint32_t)a.B;
+        blk -= (uint32_t)a.B * per;
     }
     modtable_row(a, blk, pool);
 }
 
 void launch_step_prep(const Head& h, const PrepArgs& a, bool with_mods, hipStream_t st) {
-    // The pool holds D floats (checked at create) and kModCap keys + run starts (P <= mod_cap).
-    const unsigned grid = (a.rows_dst ? 1u : 0u) + (a.hidden ? (unsigned)a.B : 0u) +
+    // The pool holds kModCap keys + run starts (P <= mod_cap) for the bias-table blocks.
+    const unsigned per = (a.D + kPrepThreads - 1u) / kPrepThreads;
+    const unsigned grid = (a.rows_dst ? 1u : 0u) + (a.hidden ? (unsigned)a.B * per : 0u) +
                           (with_mods ? (unsigned)a.B : 0u);
     if (grid == 0u) return;
     hipLaunchKernelGGL(k_step_prep, dim3(grid), dim3(kPrepThreads), 0, st, a);

@@ -45,7 +45,7 @@ constexpr uint32_t kBins = 2048;
 constexpr uint32_t kVBins = 2048;
 constexpr uint32_t kKeyCache = 8192;  // block-maximum keys kept in LDS (ntile <= 8192)
 constexpr uint32_t kRegTiles = 4096;    // block partials held in registers (kRegTiles / threads each)
-constexpr uint32_t kGatherChunk = 16384;  // shortlist gather: elements loaded per workgroup round
+constexpr uint32_t kGatherChunk = 8192;   // shortlist gather: elements loaded per workgroup round
 constexpr int kInflight = 4;          // float4 loads in flight per thread in row passes
 constexpr double kFx = 1099511627776.0;  // 2^40: fixed-point scale of histogram weights
 
@@ -735,13 +735,15 @@ __device__ inline RowCtx make_ctx(uint32_t V, const float* l, float m, float fmi
     return c;
 }
 
-// Row report and token, and the history append (src/runner.cpp:878), by thread 0.
-__device__ inline void write_row(const SelectArgs& a, uint32_t b, uint32_t token, const RowReport& rep) {
+// Row report and token, and the history append (src/runner.cpp:878), by thread 0. len: the
+// row's history length (read by the caller ahead of time), or ~0 to read it here.
+__device__ inline void write_row(const SelectArgs& a, uint32_t b, uint32_t token, const RowReport& rep,
+                                 uint32_t len = 0xFFFFFFFFu) {
     if (threadIdx.x != 0) return;
     a.tokens[b] = token;
     if (a.report) reinterpret_cast<RowReport*>(a.report)[b] = rep;
     if (a.history && a.hist_len && token != 0xFFFFFFFFu) {
-        const uint32_t len = a.hist_len[b];
+        if (len == 0xFFFFFFFFu) len = a.hist_len[b];
         if (len < a.hist_stride) {
             a.history[(size_t)b * a.hist_stride + len] = token;
             a.hist_len[b] = len + 1u;
@@ -897,27 +899,25 @@ __global__ __launch_bounds__(kMaxSelThreads) void k_fv_finish(SelectArgs a, uint
 
 // Shortlist threshold from the block-maximum keys held in registers (key[j]: tile tid + j NT,
 // 0 past ntile): a histogram of the block maxima over kWinBins value bins of width 1/32 below
-// the row maximum m. With the want-th largest block maximum in bin j (counted from m down),
-// every block counted up to bin j lies at or above m - (j + 1) w up to rounding far below one
-// bin, so m - (j + 2) w bounds the want-th largest block maximum, and with it the want-th
-// largest logit, from below. One wave scans the bins. Needs |m| <= 1024 (value rounding << w)
-// and the want-th maximum inside the window; returns 0 (not found) otherwise.
+// the row maximum m (window_add, during the row-summary pass). With the want-th largest block
+// maximum in bin j (counted from m down), every block counted up to bin j lies at or above
+// m - (j + 1) w up to rounding far below one bin, so m - (j + 2) w bounds the want-th largest
+// block maximum, and with it the want-th largest logit, from below (window_scan, one wave).
+// Needs |m| <= 1024 (value rounding << w) and the want-th maximum inside the window; the scan
+// returns 0 (not found) otherwise.
 constexpr uint32_t kWinBins = 256;
 constexpr float kWinWidth = 1.0f / 32.0f;
 template <uint32_t KP>
-__device__ __attribute__((always_inline)) inline uint32_t window_bound(SelShared& s, const uint32_t* key, float m,
-                                                                       uint32_t want) {
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    if (!(fabsf(m) <= 1024.0f)) return 0u;  // uniform
-    for (uint32_t i = tid; i < kWinBins; i += sel_nt()) s.hu[i] = 0u;
-    __syncthreads();
+__device__ __attribute__((always_inline)) inline void window_add(SelShared& s, const uint32_t* key, float m) {
 #pragma unroll
     for (uint32_t j = 0; j < KP; ++j) {
         const float v = key_float(key[j]);
         if (key[j] != 0u && v >= m - (float)kWinBins * kWinWidth)
             atomicAdd(&s.hu[min(kWinBins - 1u, (uint32_t)((m - v) * (1.0f / kWinWidth)))], 1u);
     }
-    __syncthreads();
+}
+__device__ inline uint32_t window_scan(SelShared& s, float m, uint32_t want) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     if (wave == 0u) {
         const uint4 c = *reinterpret_cast<const uint4*>(&s.hu[4u * lane]);  // bins 4 lane .. 4 lane + 3
         const uint32_t sum = c.x + c.y + c.z + c.w;
@@ -932,8 +932,7 @@ __device__ __attribute__((always_inline)) inline uint32_t window_bound(SelShared
             if (before + cl.x >= want) q = 0u;
             else if (before + cl.x + cl.y >= want) q = 1u;
             else if (before + cl.x + cl.y + cl.z >= want) q = 2u;
-            const uint32_t jb = 4u * L + q;
-            res = float_key(m - (float)(jb + 2u) * kWinWidth);
+            res = float_key(m - (float)(4u * L + q + 2u) * kWinWidth);
         }
         if (lane == 0u) s.bu[6] = res;
     }
@@ -949,29 +948,40 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
     __shared__ SelShared s;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t b = blockIdx.x;
+    // Every global load that does not depend on the row parameters is issued before anything
+    // branches on them, so the row load and these share one memory round trip.
     const DevRow row = a.rows[b];
     const float u = a.uniforms ? a.uniforms[b] : row.u;
     const BlockPartial* parts = a.partials + (size_t)b * a.ntile;
     const bool keys_cached = a.ntile <= kKeyCache;
+    const bool reg = a.ntile <= kRegTiles;
+    // register path: the partials of tiles tid + j NT, loaded without branches (indices past
+    // the last tile are clamped to it and replaced by neutral values once they arrive)
+    BlockPartial p[KP];
+#pragma unroll
+    for (uint32_t j = 0; j < KP; ++j) p[j] = parts[min(tid + j * NT, a.ntile - 1u)];
+#pragma unroll
+    for (uint32_t j = 0; j < KP; ++j)
+        if (tid + j * NT >= a.ntile) p[j] = BlockPartial{-INFINITY, 0xFFFFFFFFu, 0.0f, INFINITY};
+    // history length for the append in write_row (thread 0), fetched now
+    const uint32_t hlen = (tid == 0 && a.history && a.hist_len) ? a.hist_len[b] : 0u;
+    for (uint32_t i = tid; i < kWinBins; i += NT) s.hu[i] = 0u;  // window histogram, below
+
     // the multi-workgroup hand-over is re-armed below only for rows this step defers
     if (a.fv_part && tid == 0 && is_fv_row(row, a.V)) fv_state_of(a, b)->active = 0u;
 
+    const bool sampled = row.temperature > 0.0f;
     // 1. row max, lowest argmax, finite minimum and, for sampled rows,
     //    Z = sum_t sumexp_t * exp(max_t - m) over the block partials
-    const bool sampled = row.temperature > 0.0f;
-    const bool reg = a.ntile <= kRegTiles;
+    // shortlist rows with the keys in registers histogram them in the row-summary pass
+    const bool win = reg && sampled && row.want <= kMaxTopK && a.ntile > row.want;
     uint32_t key[KP];  // register path: block-maximum keys of tiles tid + j NT (0 past ntile)
     float m, fmin;
     uint32_t arg;
     double Z = 0.0;
     if (reg) {
-        BlockPartial p[KP];
 #pragma unroll
-        for (uint32_t j = 0; j < KP; ++j) {
-            const uint32_t t = tid + j * NT;
-            p[j] = (t < a.ntile) ? parts[t] : BlockPartial{-INFINITY, 0xFFFFFFFFu, 0.0f, INFINITY};
-            key[j] = (t < a.ntile) ? float_key(p[j].max) : 0u;
-        }
+        for (uint32_t j = 0; j < KP; ++j) key[j] = (tid + j * NT < a.ntile) ? float_key(p[j].max) : 0u;
         float bm = -INFINITY, bmin = INFINITY;
         uint32_t ba = 0xFFFFFFFFu;
 #pragma unroll
@@ -999,6 +1009,7 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
             z = wave_sum_d(z);
             if (lane == 0) s.wzs[wave] = z;
         }
+        if (win && fabsf(m) <= 1024.0f) window_add<KP>(s, key, m);
         __syncthreads();
         if (sampled && m != -INFINITY) Z = wave_sum_d(lane < sel_nw() ? s.wzs[lane] : 0.0);
     } else {
@@ -1076,7 +1087,7 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
             // histogram of the block maxima over 2048 bins of width 1/64 (the same bound over a
             // 32-unit span), and failing that the exact 22-bit key bound (two 11-bit levels).
             uint32_t tau = 0u;
-            if (a.ntile > want && reg) tau = window_bound<KP>(s, key, m, want);
+            if (win && fabsf(m) <= 1024.0f) tau = window_scan(s, m, want);
             if (a.ntile > want && tau == 0u) {
                 constexpr float kTauSpan = 32.0f;
                 constexpr float kTauInv = (float)kBins / kTauSpan;
@@ -1332,7 +1343,7 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
         }
     }
 
-    if (!deferred) write_row(a, b, token, rep);
+    if (!deferred) write_row(a, b, token, rep, hlen);
 }
 
 void launch_select(const Head& h, int batch, const SelectArgs& args, bool any_fv, hipStream_t st) {
