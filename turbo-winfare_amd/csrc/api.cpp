@@ -273,6 +273,7 @@ tdt::EpiArgs epi_args(const Head& h, float* logits, bool softcap) {
     ep.ban = nullptr;
     ep.ban_stride = 0;
     ep.rep_limit = (h.cap > 0.0f) ? h.cap * 0.9999f : 0.0f;
+    ep.no_sumexp = 1u;  // the sampling step sets 0 when a row samples from a shortlist
     return ep;
 }
 
@@ -322,7 +323,7 @@ int run_rows(HandleBox& bx, const TurboStepInputs* in, const TurboStepOutputs* o
         throw std::runtime_error("ban_stride must be at least ceil(vocab / 32) words");
 
     tdt::DevRow rows[kMaxBatch];
-    bool all_greedy = true, any_mods = false, any_fv = false;
+    bool all_greedy = true, any_mods = false, any_fv = false, any_short = false;
     for (int b = 0; b < B; ++b) {
         const TurboSamplingRow& r = in->rows[b];
         std::string why;
@@ -334,6 +335,7 @@ int run_rows(HandleBox& bx, const TurboStepInputs* in, const TurboStepOutputs* o
         all_greedy = all_greedy && r.temperature <= 0.0f;
         rows[b] = make_devrow(h, r, mods);
         any_fv = any_fv || (rows[b].temperature > 0.0f && rows[b].want >= h.V);
+        any_short = any_short || (rows[b].temperature > 0.0f && rows[b].want < h.V);
     }
     uint32_t P = 2;
     if (has_bias) P = tdt::modtable_sort_size(h, in->bias_stride);
@@ -361,6 +363,7 @@ int run_rows(HandleBox& bx, const TurboStepInputs* in, const TurboStepOutputs* o
     tdt::launch_step_prep(h, pa, any_mods, h.stream);
     release_slot(h, pos);
     tdt::EpiArgs ep = epi_args(h, logits, hidden != nullptr);
+    ep.no_sumexp = any_short ? 0u : 1u;  // greedy and full-vocabulary rows do not read them
     ep.ban = in->ban_bits;
     ep.ban_stride = in->ban_stride;
     if (hidden) launch_head(bx, B, ep);

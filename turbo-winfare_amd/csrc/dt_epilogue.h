@@ -88,8 +88,8 @@ __device__ inline void epilogue_wave(float acc, uint32_t b, uint32_t tile, uint3
     if (ep.logits && valid) ep.logits[(size_t)b * ep.V + id] = l;
     const float m = wave_max(l);
     const uint32_t arg = wave_min_u(l == m ? id : 0xFFFFFFFFu);
-    float se = (m == -INFINITY) ? 0.0f : __expf(l - m);
-    se = wave_sum(se);
+    float se = (m == -INFINITY || ep.no_sumexp) ? 0.0f : __expf(l - m);
+    if (!ep.no_sumexp) se = wave_sum(se);
     const float mn = wave_min(l == -INFINITY ? INFINITY : l);
     if (lane == 0) {
         BlockPartial bp;

@@ -97,6 +97,8 @@ struct EpiArgs {
     const uint32_t* ban;       // [B][ban_stride] or null
     uint32_t ban_stride;
     float rep_limit;           // 0.9999 * softcap used by the repetition clamp (0 = none)
+    uint32_t no_sumexp;        // 1: no row samples from a shortlist, so the block sums of
+                               // exp(l - max) are not needed and stay 0
 };
 
 enum class HeadPath { Digits, Mfma };

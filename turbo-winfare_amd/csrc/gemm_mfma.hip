@@ -340,7 +340,7 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
         const uint32_t oa = xor32(barg);
         if (om > bmax || (om == bmax && oa < barg)) { bmax = om; barg = oa; }
         float se = 0.0f;
-        if (bmax != -INFINITY) {
+        if (bmax != -INFINITY && !ep.no_sumexp) {
             const float mb2 = bmax * 1.4426950408889634f;
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb)

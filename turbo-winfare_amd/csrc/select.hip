@@ -479,6 +479,7 @@ struct FvPlan {
     uint32_t cb, dlo, dhi, u_zero;  // u_zero: u = 0 picks the first element in sorted order
     double A;                       // survivor weight (temperature) of the bins above cb
     double target_w, wabove;        // T = 1 nucleus target, and the T = 1 weight above cb
+    double total;                   // sum exp(l - m) over the row, from the T = 1 histogram
 };
 
 __device__ inline bool same_weights(const RowCtx& c) { return kLog2e / c.T == kLog2e; }
@@ -505,10 +506,10 @@ __device__ void fv_plan(SelShared& s, const RowCtx& c, float top_p, float u, FvP
     uint32_t bb;
     // nucleus bin: where the T = 1 weight reaches top_p of the row total
     uint32_t cb = kVBins;
-    double target_w = 0.0, wabove = 0.0;
+    double target_w = 0.0, wabove = 0.0, total = 0.0;
+    (void)scan_cross(s, s.vm, kVBins, INFINITY, &bb, &total);
+    P->total = total;
     if (top_p < 1.0f) {
-        double total;
-        (void)scan_cross(s, s.vm, kVBins, INFINITY, &bb, &total);
         target_w = (double)top_p * total;
         if (!scan_cross(s, s.vm, kVBins, target_w, &cb, &wabove)) cb = kVBins;
     }
@@ -682,10 +683,11 @@ __device__ int fv_finish(SelShared& s, const RowCtx& c, const FvPlan& P, uint32_
 // workgroup. Returns 1 with *token, 0 when a bin is too large to gather (radix fallback).
 __device__ __attribute__((always_inline)) inline int full_vocab_value_path(SelShared& s, const RowCtx& c, float top_p, float u,
                                      uint32_t first_id, uint32_t* token, double* denom_out,
-                                     double* r_out) {
+                                     double* r_out, double* total_out) {
     fv_hist(s, c, 0u, c.V);
     FvPlan P;
     fv_plan(s, c, top_p, u, &P);
+    *total_out = P.total;
     if (P.u_zero) {
         *token = first_id;
         *denom_out = P.A;
@@ -882,9 +884,9 @@ __global__ __launch_bounds__(kMaxSelThreads) void k_fv_finish(SelectArgs a, uint
     }
     if (!ok) {
         // too many candidates, or rounding outside the gathered bins: the one-workgroup paths
-        double dn = 0.0, rr = 0.0;
+        double dn = 0.0, rr = 0.0, zt = 0.0;
         uint32_t tk = 0;
-        if (full_vocab_value_path(s, c, st->top_p, st->u, st->arg, &tk, &dn, &rr)) {
+        if (full_vocab_value_path(s, c, st->top_p, st->u, st->arg, &tk, &dn, &rr, &zt)) {
             token = tk;
             rep.denom = dn;
             rep.r = rr;
@@ -1075,7 +1077,10 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
         rep.shortlist = want;
         bool general = (want > kMaxTopK);
         auto pkey = [&](uint32_t t) { return (keys_cached && !reg) ? s.pkey[t] : float_key(parts[t].max); };
-        if (!(Z > 0.0) || m == -INFINITY) {
+        // Full-vocabulary rows take Z from their value histogram (the head may skip the block
+        // sums of exp when no row needs them): a finite maximum is the only condition.
+        const bool fvrow = want >= a.V;
+        if (m == -INFINITY || (!fvrow && !(Z > 0.0))) {
             token = 0xFFFFFFFFu;
             rep.path = 3;
             general = false;
@@ -1305,6 +1310,7 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
                 FvPlan P;
                 fv_plan(s, c, row.top_p, u, &P);
                 FvRowState* st = fv_state_of(a, b);
+                rep.total = P.total;
                 if (P.u_zero) {
                     token = arg;
                     rep.denom = P.A;
@@ -1322,7 +1328,7 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
                     st->top_p = row.top_p;
                     st->arg = arg;
                     st->want = want;
-                    st->Z = Z;
+                    st->Z = P.total;
                     st->ncand = 0u;
                     st->overflow = 0u;
                     st->active = deferred ? 1u : 0u;
@@ -1331,7 +1337,9 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
             } else if (want >= a.V) {
                 double dn = 0.0, rr = 0.0;
                 uint32_t tk = 0;
-                if (full_vocab_value_path(s, c, row.top_p, u, arg, &tk, &dn, &rr)) {
+                const int ok = full_vocab_value_path(s, c, row.top_p, u, arg, &tk, &dn, &rr, &Z);
+                rep.total = Z;
+                if (ok) {
                     token = tk;
                     rep.denom = dn;
                     rep.r = rr;
