@@ -63,6 +63,42 @@ typedef struct {
     int device;                 /* HIP device ordinal */
 } TurboLMHeadDesc;
 
+/*
+ * ---- .gturbo bundle: resident.bin ---------------------------------------------------------
+ * One tensor of the resident index (include/gturbo/resident_index.hpp:17-27), with the
+ * quantisation geometry the reference derives from it (src/cpu_reference.cpp:229-247).
+ */
+typedef struct {
+    uint32_t dtype;             /* 0 U32 (packed quantised words), 1 BF16, 2 FP16, 3 FP32 */
+    uint32_t shape[4];
+    uint64_t file_offset, size_bytes;
+    uint64_t scale_offset, scale_size;  /* scale_size 0: not quantised */
+    uint64_t bias_offset, bias_size;
+    uint32_t quantized;
+    uint32_t rows;              /* shape[0]; 1 for an empty shape */
+    uint32_t in_dim;            /* quantised: scale_size / 2 / rows * 64; otherwise rows */
+    uint32_t bits;              /* quantised: 4 when shape[1] * 8 == in_dim, else 8; otherwise 16 */
+} TurboBundleTensor;
+
+/* Decodes the 24-byte resident header (ResidentIndexCodec::decode_header,
+ * src/resident_index.cpp:42-52): out = {index_size, resident_size, entry_count}. 1/0. */
+TURBO_DT_API int turbo_bundle_decode_header(const uint8_t* bytes, size_t count, uint64_t out[3]);
+/* Reads and validates the index region of the resident.bin at path
+ * (ResidentIndexCodec::decode_region, src/resident_index.cpp:54-104) and describes tensor
+ * `name` (ForwardRunner::resident_ref, src/runner.cpp:324-347). 1/0. */
+TURBO_DT_API int turbo_bundle_find_tensor(const char* resident_path, const char* name,
+                                          TurboBundleTensor* out);
+/*
+ * Creates the head from a bundle's resident.bin: model.embed_tokens.weight (the tied table,
+ * 4-bit, one index entry with its scale and bias regions) and model.norm.weight (BF16), read
+ * from their 16 KB-aligned regions (docs/GTURBO_FORMAT.md:26-58). The softcap and eps are the
+ * manifest's arch.final_logit_softcap and arch.rms_norm_eps (include/gturbo/manifest.hpp:34,
+ * :39), passed by the caller that parsed manifest.json. Replaces the runner's resident lookups
+ * for this path (src/runner.cpp:324-357, :722-723, :773). NULL on failure.
+ */
+TURBO_DT_API void* turbo_lmhead_create_from_bundle(const char* resident_path, float final_logit_softcap,
+                                                   float rms_norm_eps, int device);
+
 /* Fills the Gemma 4 26B-A4B constants; the four pointers are NULL. */
 TURBO_DT_API void turbo_lmhead_desc_default(TurboLMHeadDesc* out);
 
@@ -188,6 +224,25 @@ typedef struct {
  */
 TURBO_DT_API int turbo_lmhead_step(void* handle, const TurboStepInputs* in,
                                    const TurboStepOutputs* out);
+
+/*
+ * Affine-int4 matrix-vector product, out[b][r] = sum_c (q[r][c] * scale + bias) * x[b][c], at
+ * any shape a head accepts (rows up to 2^24, in_dim a multiple of 64 up to 8192): the
+ * reference's GemvInt4 (shaders/GemvInt4.hlsl:1-38) as dispatched for the q/k/v/o projections,
+ * the shared expert and the routed experts (src/runner.cpp:431-442, :621-646, :671-678). A
+ * matrix is a handle created with vocab_size = rows, hidden_size = in_dim, final_logit_softcap
+ * 0 and no norm weight. x: [batch][in_dim] (TURBO_HIDDEN_*), out: [batch][rows] FP32, device.
+ */
+TURBO_DT_API int turbo_int4_matvec(void* handle, const void* x, int x_dtype, int batch, float* out);
+
+/*
+ * Embedding lookup on the same tied table (shaders/EmbedLookup.hlsl:1-45; CPU
+ * src/cpu_reference.cpp:108-124 and :323-329): out[i] = row tokens[i] dequantised as
+ * (float)q * scale + bias, times sqrtf(hidden). tokens: [n] device ids, out: [n][hidden] FP32
+ * device, stream-ordered on the handle's stream. The reference throws for an id past the
+ * vocabulary (:325-327); here, where ids stay on the device, such a row is written as NaN.
+ */
+TURBO_DT_API int turbo_lmhead_embed(void* handle, const uint32_t* tokens, int n, float* out);
 
 /* ---- kernel-level entry points (one per reference kernel on the path) -------------------- */
 

@@ -70,6 +70,26 @@ void orc_matvec_int4(const uint8_t* W, const uint16_t* S, const uint16_t* B, uin
     }
 }
 
+void orc_embed_row(const uint8_t* W, const uint16_t* S, const uint16_t* B, uint32_t in_dim,
+                   uint32_t row, float* out) {
+    const uint32_t groups = in_dim / ORC_GROUP;
+    const uint8_t* wrow = W + (size_t)row * (in_dim / 2);
+    const uint16_t* srow = S + (size_t)row * groups;
+    const uint16_t* brow = B + (size_t)row * groups;
+    for (uint32_t g = 0; g < groups; ++g) {
+        const float s = orc_bf16_to_f32(srow[g]);
+        const float b = orc_bf16_to_f32(brow[g]);
+        for (uint32_t j = 0; j < ORC_GROUP; ++j) {
+            const uint32_t c = g * ORC_GROUP + j;
+            const uint8_t byte = wrow[c / 2];
+            const uint32_t q = (c % 2 == 0) ? (byte & 0x0Fu) : (byte >> 4u);
+            out[c] = (float)q * s + b;
+        }
+    }
+    const float scale = sqrtf((float)in_dim);
+    for (uint32_t i = 0; i < in_dim; ++i) out[i] *= scale;
+}
+
 typedef struct {
     const uint8_t* W;
     const uint16_t* S;

@@ -62,6 +62,14 @@ void orc_matvec_int4(const uint8_t* W, const uint16_t* S, const uint16_t* B, uin
 void orc_matvec_int4_mt(const uint8_t* W, const uint16_t* S, const uint16_t* B, uint32_t rows,
                         uint32_t in_dim, const float* x, float* out, int threads);
 
+/* Embedding lookup: row `row` of the tied table dequantised as (float)q * s + b, element by
+ * element in group order (src/cpu_reference.cpp:108-124, dequant_row), then every element
+ * multiplied by sqrtf((float)in_dim) (src/cpu_reference.cpp:323-329). Pinned by: a constant
+ * nibble k giving (k s + b) sqrt(D) per group, and the one-hot identity
+ * orc_matvec_int4(W, e_c)[row] == the unscaled element c (tests/test_oracle.py). */
+void orc_embed_row(const uint8_t* W, const uint16_t* S, const uint16_t* B, uint32_t in_dim,
+                   uint32_t row, float* out);
+
 /* src/cpu_reference.cpp:535-538: z = cap * tanhf(z / cap) when cap > 0. */
 void orc_softcap(float* z, size_t n, float cap);
 

@@ -78,6 +78,7 @@ def orc() -> C.CDLL:
         lib.orc_matvec_int4.argtypes = [_u8p, _u16p, _u16p, C.c_uint32, _f32p, _f32p, C.c_uint32, C.c_uint32]
         lib.orc_matvec_int4_mt.argtypes = [_u8p, _u16p, _u16p, C.c_uint32, C.c_uint32, _f32p, _f32p, C.c_int]
         lib.orc_softcap.argtypes = [_f32p, C.c_size_t, C.c_float]
+        lib.orc_embed_row.argtypes = [_u8p, _u16p, _u16p, C.c_uint32, C.c_uint32, _f32p]
         lib.orc_validate_sampling.restype = C.c_int
         lib.orc_validate_sampling.argtypes = [C.POINTER(Params), C.c_char_p, C.c_size_t]
         lib.orc_splitmix64.restype = C.c_uint64
@@ -138,6 +139,14 @@ def matvec(W, S, B, x, threads: int = 1) -> np.ndarray:
     out = np.empty(V, dtype=np.float32)
     orc().orc_matvec_int4_mt(np.ascontiguousarray(W), np.ascontiguousarray(S), np.ascontiguousarray(B),
                              V, D, np.ascontiguousarray(x, dtype=np.float32), out, threads)
+    return out
+
+
+def embed(W, S, B, token: int) -> np.ndarray:
+    """Embedding row `token` of the tied table, scaled by sqrt(hidden)."""
+    D = W.shape[1] * 2
+    out = np.empty(D, dtype=np.float32)
+    orc().orc_embed_row(np.ascontiguousarray(W), np.ascontiguousarray(S), np.ascontiguousarray(B), D, token, out)
     return out
 
 

@@ -402,3 +402,27 @@ def test_modifier_closed_forms():
     assert out[2] == np.float32(-13.0)
     assert out[3] == -np.inf                  # banned
     assert out[4] == np.float32(5.75)         # 0.5 + 0.25 summed, then added once
+
+
+def test_embed_row_closed_form_and_one_hot_matvec():
+    """Embedding lookup (src/cpu_reference.cpp:108-124, :323-329) pinned two ways: a row whose
+    nibbles are all k dequantises to (k s + b) per group, scaled by sqrtf(D); and the unscaled
+    row equals the (separately pinned) matvec against one-hot inputs, element by element."""
+    V, D = 8, 128
+    W, S, B, _ = synth.make_head(V, D, 5)
+    W = W.copy()
+    W[3, :] = 0x77  # row 3: every nibble 7
+    G = D // 64
+    sf = synth.bf16_to_f32(S).reshape(V, G)
+    bf = synth.bf16_to_f32(B).reshape(V, G)
+    scale = np.float32(np.sqrt(np.float32(D)))
+    got = O.embed(W, S, B, 3)
+    want = np.repeat((np.float32(7) * sf[3] + bf[3]).astype(np.float32), 64) * scale
+    assert np.array_equal(got, want.astype(np.float32))
+    for row in (0, 5, V - 1):
+        e = O.embed(W, S, B, row)
+        for c in (0, 1, 63, 64, D - 1):
+            x = np.zeros(D, np.float32)
+            x[c] = 1.0
+            unscaled = O.matvec(W, S, B, x)[row]
+            assert np.float32(unscaled) * scale == e[c], (row, c)

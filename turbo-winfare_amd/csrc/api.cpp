@@ -15,6 +15,7 @@
 #include <string>
 
 #include "turbo_decode_tail.h"
+#include "dt_bundle.h"
 #include "dt_internal.h"
 
 namespace tdt {
@@ -401,6 +402,33 @@ int run_rows(HandleBox& bx, const TurboStepInputs* in, const TurboStepOutputs* o
         return ret;                                      \
     }
 
+namespace {
+TurboBundleTensor describe_tensor(const tdt::ResidentEntry& e) {
+    TurboBundleTensor t{};
+    t.dtype = e.dtype;
+    for (int d = 0; d < 4; ++d) t.shape[d] = e.shape[d];
+    t.file_offset = e.file_offset;
+    t.size_bytes = e.size_bytes;
+    t.scale_offset = e.scale_offset;
+    t.scale_size = e.scale_size;
+    t.bias_offset = e.bias_offset;
+    t.bias_size = e.bias_size;
+    // src/cpu_reference.cpp:229-247 (an all-zero shape reads as rows = shape[0] = 0 there too)
+    t.rows = e.shape[0];
+    t.quantized = e.scale_size > 0 ? 1u : 0u;
+    if (t.quantized) {
+        if (t.rows == 0) throw std::runtime_error(e.name + ": quantised tensor with zero rows");
+        const uint64_t groups = e.scale_size / 2u / t.rows;
+        t.in_dim = static_cast<uint32_t>(groups * 64u);
+        t.bits = (static_cast<uint64_t>(e.shape[1]) * 8u == t.in_dim) ? 4u : 8u;
+    } else {
+        t.in_dim = t.rows;
+        t.bits = 16u;
+    }
+    return t;
+}
+}  // namespace
+
 extern "C" {
 
 TURBO_DT_API const char* turbo_lmhead_last_error(void) { return g_last_error.c_str(); }
@@ -750,4 +778,86 @@ TURBO_DT_API int turbo_lmhead_head_kernel_time(void* handle, double* total_ms, i
     API_CATCH(0)
 }
 
+
+TURBO_DT_API int turbo_int4_matvec(void* handle, const void* x, int x_dtype, int batch, float* out) {
+    return turbo_lmhead_logits(handle, x, x_dtype, batch, 0, out);
+}
+
+TURBO_DT_API int turbo_lmhead_embed(void* handle, const uint32_t* tokens, int n, float* out) {
+    clear_error();
+    API_TRY
+    HandleBox* bx = box(handle);
+    Head& h = bx->h;
+    check_hip(hipSetDevice(h.device), "hipSetDevice");
+    if (n < 0) throw std::runtime_error("n must be >= 0");
+    if (n > 0 && (!tokens || !out)) throw std::runtime_error("tokens or out is NULL");
+    if (n > 65535 * 16) throw std::runtime_error("at most 1048560 tokens per call");
+    // src/cpu_reference.cpp:328: the scale is sqrt of the hidden size in float
+    tdt::launch_embed(h, tokens, n, out, std::sqrt(static_cast<float>(h.D)), h.stream);
+    return 1;
+    API_CATCH(0)
+}
+
+TURBO_DT_API int turbo_bundle_decode_header(const uint8_t* bytes, size_t count, uint64_t out[3]) {
+    clear_error();
+    API_TRY
+    if (!bytes || !out) throw std::runtime_error("bytes or out is NULL");
+    const tdt::ResidentHeader h = tdt::decode_resident_header(bytes, count);
+    out[0] = h.index_size;
+    out[1] = h.resident_size;
+    out[2] = h.entry_count;
+    return 1;
+    API_CATCH(0)
+}
+
+
+TURBO_DT_API int turbo_bundle_find_tensor(const char* resident_path, const char* name, TurboBundleTensor* out) {
+    clear_error();
+    API_TRY
+    if (!resident_path || !name || !out) throw std::runtime_error("path, name or out is NULL");
+    *out = describe_tensor(tdt::find_resident_tensor(resident_path, name, nullptr));
+    return 1;
+    API_CATCH(0)
+}
+
+TURBO_DT_API void* turbo_lmhead_create_from_bundle(const char* resident_path, float final_logit_softcap,
+                                                   float rms_norm_eps, int device) {
+    clear_error();
+    API_TRY
+    if (!resident_path) throw std::runtime_error("resident_path is NULL");
+    const std::string path(resident_path);
+    const tdt::ResidentEntry ee = tdt::find_resident_tensor(path, "model.embed_tokens.weight", nullptr);
+    const tdt::ResidentEntry ne = tdt::find_resident_tensor(path, "model.norm.weight", nullptr);
+    const TurboBundleTensor et = describe_tensor(ee);
+    if (!et.quantized || et.bits != 4u)
+        throw std::runtime_error("model.embed_tokens.weight: expected a 4-bit quantised tensor");
+    const uint64_t V = et.rows, D = et.in_dim, G = D / 64u;
+    if (V == 0 || D == 0) throw std::runtime_error("model.embed_tokens.weight: empty shape");
+    if (ee.size_bytes < V * (D / 2u) || ee.scale_size != V * G * 2u || ee.bias_size != V * G * 2u)
+        throw std::runtime_error("model.embed_tokens.weight: region sizes do not match its shape");
+    if (ne.dtype != 1u || ne.size_bytes < D * 2u)
+        throw std::runtime_error("model.norm.weight: expected " + std::to_string(D) + " BF16 values");
+    std::vector<uint8_t> W(static_cast<size_t>(V * (D / 2u)));
+    std::vector<uint16_t> S(static_cast<size_t>(V * G)), B(static_cast<size_t>(V * G)), g(static_cast<size_t>(D));
+    tdt::read_file_region(path, ee.file_offset, W.size(), W.data());
+    tdt::read_file_region(path, ee.scale_offset, S.size() * 2u, S.data());
+    tdt::read_file_region(path, ee.bias_offset, B.size() * 2u, B.data());
+    tdt::read_file_region(path, ne.file_offset, g.size() * 2u, g.data());
+    TurboLMHeadDesc d;
+    turbo_lmhead_desc_default(&d);
+    d.vocab_size = static_cast<uint32_t>(V);
+    d.hidden_size = static_cast<uint32_t>(D);
+    d.final_logit_softcap = final_logit_softcap;
+    d.rms_norm_eps = rms_norm_eps;
+    d.weights_on_device = 0;
+    d.weight = W.data();
+    d.scales = S.data();
+    d.biases = B.data();
+    d.norm_weight = g.data();
+    d.device = device;
+    void* h = turbo_lmhead_create(&d);
+    if (!h) throw std::runtime_error(g_last_error);
+    return h;
+    API_CATCH(nullptr)
+}
 }  // extern "C"

@@ -190,6 +190,8 @@ void launch_select(const Head& h, int batch, const SelectArgs& a, bool any_fv, h
 void launch_softcap(float* z, size_t n, float cap, hipStream_t st);
 void launch_repetition(float* logits, uint32_t vocab, const uint32_t* history, uint32_t n,
                        float penalty, float softcap, hipStream_t st);
+// out[i][D] = row tokens[i] of the tied table dequantised and scaled by `scale` (NaN past V).
+void launch_embed(const Head& h, const uint32_t* tokens, int n, float* out, float scale, hipStream_t st);
 
 // Throws std::runtime_error with the HIP error string on failure.
 void check_hip(hipError_t e, const char* what);

@@ -17,6 +17,8 @@
 //  * Loads are nontemporal and software-pipelined kPF groups ahead.
 #include <hip/hip_ext.h>
 
+#include <algorithm>
+
 #include "dt_epilogue.h"
 
 namespace tdt {
@@ -112,8 +114,82 @@ __global__ __launch_bounds__(kDigitWaves * 64) void k_head_digits(
     for (int nb = 0; nb < NB; ++nb) epilogue_wave(acc[nb], (uint32_t)nb, tile, lane, ep);
 }
 
+// Matrices with few 64-row tiles (the projection shapes) give one wave per tile too little
+// parallelism: here a workgroup of KS waves shares one tile, wave w taking groups
+// [w G / KS, (w + 1) G / KS), and the partial sums are added in wave order through LDS before
+// wave 0 runs the epilogue.
+constexpr uint32_t kMaxSplit = 16;
+template <int NB>
+__global__ __launch_bounds__(kMaxSplit * 64) void k_head_digits_split(
+    const uint4* __restrict__ Wt, const uint32_t* __restrict__ SBt, const uint32_t* __restrict__ xdig,
+    const float* __restrict__ xws, const float* __restrict__ xsum, uint32_t NC, uint32_t G, EpiArgs ep) {
+    __shared__ float part[kMaxSplit][NB][64];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, KS = blockDim.x >> 6;
+    const uint32_t tile = blockIdx.x;
+    const uint4* wp = Wt + (size_t)tile * NC * kTileRows + lane;
+    const uint32_t* sbp = SBt + (size_t)tile * G * kTileRows + lane;
+    float acc[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[nb] = 0.0f;
+    const uint32_t g0 = wave * G / KS, g1 = (wave + 1u) * G / KS;
+    for (uint32_t g = g0; g < g1; ++g) {
+        const uint4 A = load_stream(wp + (size_t)(2 * g) * kTileRows);
+        const uint4 Bw = load_stream(wp + (size_t)(2 * g + 1) * kTileRows);
+        const uint32_t sbw = load_stream(sbp + (size_t)g * kTileRows);
+        const uint32_t wq[8] = {A.x ^ 0x88888888u, A.y ^ 0x88888888u, A.z ^ 0x88888888u,
+                                A.w ^ 0x88888888u, Bw.x ^ 0x88888888u, Bw.y ^ 0x88888888u,
+                                Bw.z ^ 0x88888888u, Bw.w ^ 0x88888888u};
+        const float sf = bf16_to_f32(sbw & 0xFFFFu);
+        const float bf = bf16_to_f32(sbw >> 16);
+        const float c8 = fmaf(8.0f, sf, bf);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            const uint32_t* xd = xdig + ((size_t)nb * NC + 2u * g) * kDigitWordsPerChunk;
+            int a[kDigits];
+#pragma unroll
+            for (uint32_t k = 0; k < kDigits; ++k) a[k] = 0;
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (uint32_t k = 0; k < kDigits; ++k)
+                        a[k] = __builtin_amdgcn_sdot8((int)wq[4 * hh + i],
+                                                      (int)xd[hh * kDigitWordsPerChunk + k * 4 + i], a[k], false);
+            uint32_t Dg = (uint32_t)a[0];
+#pragma unroll
+            for (uint32_t k = 1; k < kDigits; ++k) Dg += (uint32_t)a[k] << (4u * k);
+            acc[nb] = fmaf((float)(int)Dg, sf * xws[(size_t)nb * G + g], acc[nb]);
+            acc[nb] = fmaf(c8, xsum[(size_t)nb * G + g], acc[nb]);
+        }
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) part[wave][nb][lane] = acc[nb];
+    __syncthreads();
+    if (wave != 0u) return;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        float v = part[0][nb][lane];
+        for (uint32_t w = 1; w < KS; ++w) v += part[w][nb][lane];
+        epilogue_wave(v, (uint32_t)nb, tile, lane, ep);
+    }
+}
+
 void launch_head_digits(const Head& h, int batch, const EpiArgs& ep, hipStream_t st,
                         hipEvent_t ev0, hipEvent_t ev1) {
+    // enough waves to fill the chip (~2048) from few tiles: split each tile's groups
+    const uint32_t ks = std::min<uint32_t>({kMaxSplit, h.G, (2048u + h.ntile - 1u) / h.ntile});
+    if (ks >= 2u && (batch == 1 || batch == 2)) {
+        const dim3 grid(h.ntile), block(64u * ks);
+        if (batch == 1)
+            hipExtLaunchKernelGGL(k_head_digits_split<1>, grid, block, 0, st, ev0, ev1, 0, h.Wt, h.SBt, h.xdig,
+                                  h.xws, h.xsum, h.NC, h.G, ep);
+        else
+            hipExtLaunchKernelGGL(k_head_digits_split<2>, grid, block, 0, st, ev0, ev1, 0, h.Wt, h.SBt, h.xdig,
+                                  h.xws, h.xsum, h.NC, h.G, ep);
+        check_hip(hipGetLastError(), "head (digit GEMV, split groups)");
+        return;
+    }
     const unsigned grid = (h.ntile + kDigitWaves - 1) / kDigitWaves;
     if (batch == 1)
         hipExtLaunchKernelGGL(k_head_digits<1>, dim3(grid), dim3(kDigitWaves * 64), 0, st, ev0, ev1,

@@ -75,4 +75,45 @@ void launch_repetition(float* logits, uint32_t vocab, const uint32_t* history, u
     check_hip(hipGetLastError(), "repetition penalty");
 }
 
+// ---- embedding lookup ------------------------------------------------------------------------
+// Row `id` of the tied table from the head's tiled copy, dequantised as (float)q * s + b and
+// scaled by sqrtf(D) (src/cpu_reference.cpp:108-124, :323-329; shaders/EmbedLookup.hlsl:32-44).
+// One workgroup per token; a thread handles one packed word (8 nibbles) at a time: chunk c of
+// row r in tile t is the uint4 Wt[(t NC + c) 64 + r], its word j holds elements 32c + 8j ...
+// low nibble first. Ids past the vocabulary give a row of NaN.
+__global__ __launch_bounds__(256) void k_embed(const uint32_t* __restrict__ Wt, const uint32_t* __restrict__ SBt,
+                                               uint32_t V, uint32_t D, uint32_t NC, uint32_t G, float scale,
+                                               const uint32_t* __restrict__ tokens, float* __restrict__ out) {
+#pragma clang fp contract(off)
+    const uint32_t id = tokens[blockIdx.x];
+    float* dst = out + (size_t)blockIdx.x * D;
+    const uint32_t tile = id >> 6, r = id & 63u;
+    for (uint32_t w = threadIdx.x; w < D / 8u; w += blockDim.x) {
+        float v[8];
+        if (id < V) {
+            const uint32_t word = Wt[(((size_t)tile * NC + (w >> 2)) * kTileRows + r) * 4u + (w & 3u)];
+            const uint32_t sb = SBt[((size_t)tile * G + (w >> 3)) * kTileRows + r];
+            const float s = bf16_to_f32(sb & 0xFFFFu), b = bf16_to_f32(sb >> 16);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float x = (float)((word >> (4 * e)) & 15u) * s;
+                x = x + b;
+                v[e] = x * scale;
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = __builtin_nanf("");
+        }
+        reinterpret_cast<float4*>(dst + 8u * w)[0] = make_float4(v[0], v[1], v[2], v[3]);
+        reinterpret_cast<float4*>(dst + 8u * w)[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+}
+
+void launch_embed(const Head& h, const uint32_t* tokens, int n, float* out, float scale, hipStream_t st) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(k_embed, dim3((unsigned)n), dim3(256), 0, st, reinterpret_cast<const uint32_t*>(h.Wt),
+                       h.SBt, h.V, h.D, h.NC, h.G, scale, tokens, out);
+    check_hip(hipGetLastError(), "embedding lookup");
+}
+
 }  // namespace tdt

@@ -45,6 +45,11 @@ EXPORTS = (
     "turbo_sample_logits",
     "turbo_lmhead_enable_head_timing",
     "turbo_lmhead_head_kernel_time",
+    "turbo_int4_matvec",
+    "turbo_lmhead_embed",
+    "turbo_bundle_decode_header",
+    "turbo_bundle_find_tensor",
+    "turbo_lmhead_create_from_bundle",
 )
 
 
@@ -122,6 +127,23 @@ class TurboStepOutputs(C.Structure):
     ]
 
 
+class TurboBundleTensor(C.Structure):
+    _fields_ = [
+        ("dtype", C.c_uint32),
+        ("shape", C.c_uint32 * 4),
+        ("file_offset", C.c_uint64),
+        ("size_bytes", C.c_uint64),
+        ("scale_offset", C.c_uint64),
+        ("scale_size", C.c_uint64),
+        ("bias_offset", C.c_uint64),
+        ("bias_size", C.c_uint64),
+        ("quantized", C.c_uint32),
+        ("rows", C.c_uint32),
+        ("in_dim", C.c_uint32),
+        ("bits", C.c_uint32),
+    ]
+
+
 _lib = None
 
 
@@ -159,6 +181,11 @@ def load(path: os.PathLike | str | None = None) -> C.CDLL:
         "turbo_sample_logits": (i32, [vp, vp, C.POINTER(TurboStepInputs), C.POINTER(TurboStepOutputs)]),
         "turbo_lmhead_enable_head_timing": (i32, [vp, i32]),
         "turbo_lmhead_head_kernel_time": (i32, [vp, C.POINTER(C.c_double), C.POINTER(i32), i32]),
+        "turbo_int4_matvec": (i32, [vp, vp, i32, i32, vp]),
+        "turbo_lmhead_embed": (i32, [vp, vp, i32, vp]),
+        "turbo_bundle_decode_header": (i32, [vp, C.c_size_t, C.POINTER(C.c_uint64)]),
+        "turbo_bundle_find_tensor": (i32, [C.c_char_p, C.c_char_p, C.POINTER(TurboBundleTensor)]),
+        "turbo_lmhead_create_from_bundle": (vp, [C.c_char_p, f32, f32, i32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -205,8 +232,35 @@ def _ptr(t) -> int | None:
     return int(t.data_ptr()) if hasattr(t, "data_ptr") else int(t)
 
 
+def bundle_decode_header(data: bytes) -> tuple[int, int, int]:
+    """(index_size, resident_size, entry_count) of a resident.bin header."""
+    out = (C.c_uint64 * 3)()
+    buf = C.create_string_buffer(bytes(data), len(data))
+    _ok(load().turbo_bundle_decode_header(C.addressof(buf), len(data), out))
+    return int(out[0]), int(out[1]), int(out[2])
+
+
+def bundle_find_tensor(resident_path, name: str) -> TurboBundleTensor:
+    t = TurboBundleTensor()
+    _ok(load().turbo_bundle_find_tensor(str(resident_path).encode(), name.encode(), C.byref(t)))
+    return t
+
+
 class LMHead:
     """Owns one turbo_lmhead handle. Arrays: numpy (host) or torch CUDA tensors (device)."""
+
+    @classmethod
+    def from_bundle(cls, resident_path, *, softcap: float = 30.0, eps: float = 1e-6, device: int = 0):
+        """Head from a .gturbo bundle's resident.bin (model.embed_tokens.weight + model.norm.weight)."""
+        self = cls.__new__(cls)
+        self.lib = load()
+        h = self.lib.turbo_lmhead_create_from_bundle(str(resident_path).encode(), softcap, eps, device)
+        if not h:
+            raise TurboError(last_error())
+        t = bundle_find_tensor(resident_path, "model.embed_tokens.weight")
+        self.vocab, self.hidden = int(t.rows), int(t.in_dim)
+        self.h = h
+        return self
 
     def __init__(self, weight, scales, biases, norm_weight=None, *, vocab: int, hidden: int,
                  softcap: float = 30.0, eps: float = 1e-6, on_device: bool = False, device: int = 0):
@@ -255,6 +309,14 @@ class LMHead:
 
     def rms_norm(self, x, batch: int, out) -> None:
         _ok(self.lib.turbo_lmhead_rms_norm(self.h, _ptr(x), batch, _ptr(out)))
+
+    def matvec(self, x, batch: int, out, *, dtype: int = TURBO_HIDDEN_F32) -> None:
+        """out[b][r] = sum_c w[r][c] x[b][c] (no norm, no softcap); device buffers."""
+        _ok(self.lib.turbo_int4_matvec(self.h, _ptr(x), dtype, batch, _ptr(out)))
+
+    def embed(self, tokens, n: int, out) -> None:
+        """out[i] = embedding row tokens[i] (dequantised, times sqrt(hidden)); device buffers."""
+        _ok(self.lib.turbo_lmhead_embed(self.h, _ptr(tokens), n, _ptr(out)))
 
     def logits(self, x, batch: int, out, *, dtype: int = TURBO_HIDDEN_F32, softcap: bool = True) -> None:
         _ok(self.lib.turbo_lmhead_logits(self.h, _ptr(x), dtype, batch, 1 if softcap else 0, _ptr(out)))
