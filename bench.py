@@ -11,7 +11,8 @@ are resident in HBM before the timed region.
 
 The JSON line also reports the same head at B = 32 (mixed per-row parameters with
 presence/frequency penalties over 1024-id Zipf histories) and B = 256 (full-vocabulary top-p
-0.9 on bf16 hidden states), each with its head kernel's roofline.
+0.9 on bf16 hidden states), each with its head kernel's roofline, and ("widened") the int4
+matvec at the reference's projection shapes and the embedding lookup.
 
 roofline: the dominant kernel is the head (int4 GEMV at B <= 2, MFMA at B > 2). Its average
 duration is measured during the timed region with HIP start/stop events of the kernel's own
@@ -148,6 +149,46 @@ def batched_line(T, torch, head, B, warm, steps):
     return out
 
 
+def widened_lines(T, torch):
+    """Rows beyond the decode tail that share its kernels: the int4 matvec at the reference's
+    projection shapes (B = 1; digit GEMV, split over the groups of each 64-row tile) and the
+    embedding lookup on the tied table. Kernel times come from the head's dispatch events on
+    every call; call times are wall clock per call (prep + kernel launches included)."""
+    import synth
+    out = {"matvec_b1": {}, "embed": {}}
+    for rows, k in [(704, 2816), (2816, 704), (2112, 2816), (2816, 2112), (4096, 2816)]:
+        W, S, B, _ = synth.make_head(rows, k, rows + k)
+        h = T.LMHead(W, S, B, None, vocab=rows, hidden=k, softcap=0.0)
+        x = torch.from_numpy(synth.hidden_states(1, k, 3)).cuda()
+        o = torch.empty((1, rows), dtype=torch.float32, device="cuda")
+        for _ in range(20):
+            h.matvec(x, 1, o)
+        h.enable_head_timing(True, every=1)
+        h.head_kernel_time(reset=True)
+        n = 200
+        el = time_loop(torch, lambda s: h.matvec(x, 1, o), 0, n)
+        kms, cnt = h.head_kernel_time(reset=True)
+        kus = 1e3 * kms / max(cnt, 1)
+        byts = rows * k // 2 + rows * (k // 64) * 4 + k * 4 + rows * 4
+        out["matvec_b1"][f"{rows}x{k}"] = {"kernel_us": kus, "call_us": 1e6 * el / n,
+                                           "kernel_GBs": byts / (kus * 1e-6) / 1e9,
+                                           "algorithmic_bytes": byts}
+        h.close()
+    W, S, B, g = synth.make_head(V, D, SEED)
+    h = T.LMHead(W, S, B, g, vocab=V, hidden=D)
+    for ntok in (1, 256):
+        ids = torch.from_numpy((np.arange(ntok, dtype=np.int64) * 1021 % V).astype(np.int32)).cuda()
+        e = torch.empty((ntok, D), dtype=torch.float32, device="cuda")
+        for _ in range(20):
+            h.embed(ids, ntok, e)
+        n = 500
+        el = time_loop(torch, lambda s: h.embed(ids, ntok, e), 0, n)
+        byts = ntok * (D // 2 + (D // 64) * 4 + D * 4)
+        out["embed"][f"{ntok}_tokens"] = {"call_us": 1e6 * el / n, "algorithmic_bytes": byts}
+    h.close()
+    return out
+
+
 def cpu_baseline(W, S, B, g, nsteps):
     """Oracle restatement of the reference CPU path for config-2 steps on this host."""
     import orc_py as O
@@ -251,6 +292,9 @@ def main():
         line["batches"] = {"B32": batched_line(T, torch, head, 32, 10, 96),
                            "B256": batched_line(T, torch, head, 256, 5, 64)}
     head.close()
+    if not a.no_batches and a.only is None:
+        log("matvec shapes and embedding lookup")
+        line["widened"] = widened_lines(T, torch)
     if not a.no_cpu and a.only is None:
         log("cpu baseline")
         line["cpu_baseline"] = cpu_baseline(W, S, B, g, a.cpu_steps)

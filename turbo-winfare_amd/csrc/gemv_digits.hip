@@ -124,7 +124,10 @@ __global__ __launch_bounds__(kMaxSplit * 64) void k_head_digits_split(
     const uint4* __restrict__ Wt, const uint32_t* __restrict__ SBt, const uint32_t* __restrict__ xdig,
     const float* __restrict__ xws, const float* __restrict__ xsum, uint32_t NC, uint32_t G, EpiArgs ep) {
     __shared__ float part[kMaxSplit][NB][64];
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, KS = blockDim.x >> 6;
+    // wave-uniform by construction; read through the scalar unit so the group range, and with it
+    // the digit-word addresses, stay scalar (s_load) instead of per-lane loads
+    const uint32_t lane = threadIdx.x & 63u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t KS = blockDim.x >> 6;
     const uint32_t tile = blockIdx.x;
     const uint4* wp = Wt + (size_t)tile * NC * kTileRows + lane;
     const uint32_t* sbp = SBt + (size_t)tile * G * kTileRows + lane;
@@ -132,35 +135,54 @@ __global__ __launch_bounds__(kMaxSplit * 64) void k_head_digits_split(
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[nb] = 0.0f;
     const uint32_t g0 = wave * G / KS, g1 = (wave + 1u) * G / KS;
-    for (uint32_t g = g0; g < g1; ++g) {
-        const uint4 A = load_stream(wp + (size_t)(2 * g) * kTileRows);
-        const uint4 Bw = load_stream(wp + (size_t)(2 * g + 1) * kTileRows);
-        const uint32_t sbw = load_stream(sbp + (size_t)g * kTileRows);
-        const uint32_t wq[8] = {A.x ^ 0x88888888u, A.y ^ 0x88888888u, A.z ^ 0x88888888u,
-                                A.w ^ 0x88888888u, Bw.x ^ 0x88888888u, Bw.y ^ 0x88888888u,
-                                Bw.z ^ 0x88888888u, Bw.w ^ 0x88888888u};
-        const float sf = bf16_to_f32(sbw & 0xFFFFu);
-        const float bf = bf16_to_f32(sbw >> 16);
-        const float c8 = fmaf(8.0f, sf, bf);
+    // a wave holds few groups: all of a batch of kBatchG are loaded before any is used, so
+    // the wave waits for memory once per batch rather than once per group
+    constexpr uint32_t kBatchG = 4;
+    for (uint32_t gb = g0; gb < g1; gb += kBatchG) {
+        uint4 Ab[kBatchG], Bb[kBatchG];
+        uint32_t Sb[kBatchG];
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            const uint32_t* xd = xdig + ((size_t)nb * NC + 2u * g) * kDigitWordsPerChunk;
-            int a[kDigits];
+        for (uint32_t q = 0; q < kBatchG; ++q) {
+            const uint32_t g = min(gb + q, g1 - 1u);  // past the range: a repeated, unused load
+            Ab[q] = load_stream(wp + (size_t)(2 * g) * kTileRows);
+            Bb[q] = load_stream(wp + (size_t)(2 * g + 1) * kTileRows);
+            Sb[q] = load_stream(sbp + (size_t)g * kTileRows);
+        }
 #pragma unroll
-            for (uint32_t k = 0; k < kDigits; ++k) a[k] = 0;
+        for (uint32_t q = 0; q < kBatchG; ++q) {
+            // branch-free: a group past the range is computed on its clamped copy and dropped,
+            // so no branch separates the batch's loads from each other
+            const bool in = gb + q < g1;
+            const uint32_t g = min(gb + q, g1 - 1u);
+            const uint4 A = Ab[q], Bw = Bb[q];
+            const uint32_t sbw = Sb[q];
+            const uint32_t wq[8] = {A.x ^ 0x88888888u, A.y ^ 0x88888888u, A.z ^ 0x88888888u,
+                                    A.w ^ 0x88888888u, Bw.x ^ 0x88888888u, Bw.y ^ 0x88888888u,
+                                    Bw.z ^ 0x88888888u, Bw.w ^ 0x88888888u};
+            const float sf = bf16_to_f32(sbw & 0xFFFFu);
+            const float bf = bf16_to_f32(sbw >> 16);
+            const float c8 = fmaf(8.0f, sf, bf);
 #pragma unroll
-            for (int hh = 0; hh < 2; ++hh)
+            for (int nb = 0; nb < NB; ++nb) {
+                const uint32_t* xd = xdig + ((size_t)nb * NC + 2u * g) * kDigitWordsPerChunk;
+                int a[kDigits];
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+                for (uint32_t k = 0; k < kDigits; ++k) a[k] = 0;
 #pragma unroll
-                    for (uint32_t k = 0; k < kDigits; ++k)
-                        a[k] = __builtin_amdgcn_sdot8((int)wq[4 * hh + i],
-                                                      (int)xd[hh * kDigitWordsPerChunk + k * 4 + i], a[k], false);
-            uint32_t Dg = (uint32_t)a[0];
+                for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-            for (uint32_t k = 1; k < kDigits; ++k) Dg += (uint32_t)a[k] << (4u * k);
-            acc[nb] = fmaf((float)(int)Dg, sf * xws[(size_t)nb * G + g], acc[nb]);
-            acc[nb] = fmaf(c8, xsum[(size_t)nb * G + g], acc[nb]);
+                    for (int i = 0; i < 4; ++i)
+#pragma unroll
+                        for (uint32_t k = 0; k < kDigits; ++k)
+                            a[k] = __builtin_amdgcn_sdot8((int)wq[4 * hh + i],
+                                                          (int)xd[hh * kDigitWordsPerChunk + k * 4 + i], a[k], false);
+                uint32_t Dg = (uint32_t)a[0];
+#pragma unroll
+                for (uint32_t k = 1; k < kDigits; ++k) Dg += (uint32_t)a[k] << (4u * k);
+                float t = fmaf((float)(int)Dg, sf * xws[(size_t)nb * G + g], acc[nb]);
+                t = fmaf(c8, xsum[(size_t)nb * G + g], t);
+                acc[nb] = in ? t : acc[nb];
+            }
         }
     }
 #pragma unroll
