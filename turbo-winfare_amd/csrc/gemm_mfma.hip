@@ -19,9 +19,9 @@
 //    activations are stored k-permuted within each octet as (x0, x4, x1, x5, x2, x6, x3, x7)
 //    to match the order the dequant produces halves in.
 //  * Workgroup = 4 waves, one 64-row tile each, over a block of 32*NB batch columns
-//    (blockIdx.y: B = 256 runs two column blocks). Weights are prefetched PF groups ahead into
-//    registers; activations for group g+1 are staged through registers into the other half of a
-//    double-buffered LDS tile while group g computes, one barrier per group.
+//    (blockIdx.y: B = 256 runs two column blocks). Weights and activations are prefetched PF
+//    groups ahead into registers; the activations of group g+1 are written into the other half
+//    of a double-buffered LDS tile at the end of group g, one barrier per group.
 //  * Epilogue in place on the accumulators: per (column, 64-row tile), lane-local reductions
 //    and one cross-lane exchange give the block partial; logits leave as float4 stores.
 #include <hip/hip_ext.h>
@@ -160,17 +160,20 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[mb][nb][r] = 0.0f;
 
+    // Weights and activations are prefetched PF groups ahead in the same slots, in the same
+    // order: the load counter is in-order, so waiting for a group's activations (at the LDS
+    // store) only waits for loads that the next group needs anyway.
     uint4 wr[PF][2];
     uint32_t sbr[PF][2];
+    v4u xr[PF][XPT];
 #pragma unroll
     for (int p = 0; p < PF; ++p) {
         const uint32_t gp = min((uint32_t)p, G - 1u);
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb) { wr[p][mb] = wload(gp, mb); sbr[p][mb] = sload(gp, mb); }
+        load_x(gp, xr[p]);
     }
-    v4u xr[XPT];
-    load_x(0, xr);
-    store_x(0, xr);
+    store_x(0, xr[0]);
     __syncthreads();
 
     h8v acur[2], anext[2];
@@ -188,10 +191,11 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
             SbHalves hc[2];
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb) { wc[mb] = wr[p][mb]; hc[mb] = unpack_sb(sbr[p][mb]); }
-            load_x(min(g + 1u, G - 1u), xr);
+            // slot p held group g, whose activations are already in LDS: refill it with g + PF
             const uint32_t gn = min(g + (uint32_t)PF, G - 1u);
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb) { wr[p][mb] = wload(gn, mb); sbr[p][mb] = sload(gn, mb); }
+            load_x(gn, xr[p]);
             constexpr int kNext = (PF > 1) ? 1 : 0;
             const int pn = (p + kNext) % PF;         // prefetch slot holding group g + 1
             const _Float16* lb = &lx[buf][0];
@@ -224,7 +228,7 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
 #pragma unroll
                 for (int mb = 0; mb < 2; ++mb) acur[mb] = anext[mb];
             }
-            store_x(buf ^ 1u, xr);
+            store_x(buf ^ 1u, xr[(p + 1) % PF]);  // group g + 1 (clamped), loaded PF - 1 groups ago
             __syncthreads();
             buf ^= 1u;
         }
