@@ -336,10 +336,11 @@ def test_full_vocab_rows_split_over_workgroups(head):
         assert all(paths[b] == 2 for b in live), paths
 
 
-@pytest.mark.parametrize("batch", [3, 12])
-def test_back_to_back_steps_match_synchronised(head, batch):
+@pytest.mark.parametrize("batch,fv", [(3, False), (12, False), (12, True)])
+def test_back_to_back_steps_match_synchronised(head, batch, fv):
     """Row parameters reach the kernels through the kernel arguments (batches up to 8) or a
-    pinned ring whose slots are refilled group by group. Many steps enqueued back to back, each
+    pinned ring whose slots are refilled group by group, and full-vocabulary rows leave their
+    summed slice histograms cleared for the next step. Many steps enqueued back to back, each
     with its own temperature, top-k and uniform, must give exactly the tokens of the same steps
     run one at a time with a synchronisation after each (where no slot can be reused early)."""
     h, _ = head
@@ -348,8 +349,14 @@ def test_back_to_back_steps_match_synchronised(head, batch):
     tok_all = torch.zeros((steps, batch), dtype=torch.int32, device="cuda")
 
     def rows_for(s):
-        return [T.row_default(temperature=0.4 + 0.05 * ((s + b) % 9), top_k=[0, 1, 5, 40][(s + b) % 4] or 64,
+        rows = [T.row_default(temperature=0.4 + 0.05 * ((s + b) % 9), top_k=[0, 1, 5, 40][(s + b) % 4] or 64,
                               top_p=0.9, seed=77 + b, counter=s) for b in range(batch)]
+        if fv:  # every third row samples the whole vocabulary (the multi-workgroup path, whose
+            # histogram sums must be back at zero for the next step)
+            for b in range(0, batch, 3):
+                rows[b] = T.row_default(temperature=0.7 + 0.1 * (s % 3), top_k=0, top_p=0.85, seed=91 + b,
+                                        counter=s, flags=T.TURBO_ROW_FULL_VOCAB)
+        return rows
 
     keep = []
     for s in range(steps):  # back to back

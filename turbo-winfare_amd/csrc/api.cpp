@@ -156,7 +156,7 @@ void free_head(Head& h) {
     dfree(h.hcount);
     dfree(h.hbits);
     dfree(h.list_scratch);
-    dfree(h.fv_part);
+    dfree(h.fv_acc);
     dfree(h.fv_merged);
     dfree(h.fv_cand);
     dfree(h.fv_state);
@@ -529,8 +529,10 @@ TURBO_DT_API void* turbo_lmhead_create(const TurboLMHeadDesc* d) {
         check_hip(hipMemset(h.hcount, 0, MB * h.V * sizeof(uint32_t)), "clear history counts");
         check_hip(hipMemset(h.hbits, 0, MB * h.hbw * sizeof(uint32_t)), "clear history bitmap");
         h.list_scratch = dalloc<uint2>(MB * h.V, "alloc list scratch");
-        h.fv_part = dalloc<unsigned long long>((size_t)tdt::kFvMaxBatch * tdt::kFvSlices * 2u * tdt::kFvBins,
-                                               "alloc select slice histograms");
+        h.fv_acc = dalloc<unsigned long long>((size_t)tdt::kFvMaxBatch * 2u * tdt::kFvBins,
+                                              "alloc select slice-histogram sums");
+        check_hip(hipMemset(h.fv_acc, 0, (size_t)tdt::kFvMaxBatch * 2u * tdt::kFvBins * 8u),
+                  "clear select slice-histogram sums");
         h.fv_merged = dalloc<unsigned long long>((size_t)tdt::kFvMaxBatch * 2u * tdt::kFvBins, "alloc select histograms");
         h.fv_cand = dalloc<unsigned long long>((size_t)tdt::kFvMaxBatch * tdt::kFvCandCap, "alloc select candidates");
         h.fv_state = dalloc<unsigned char>((size_t)tdt::kFvMaxBatch * tdt::kFvStateBytes, "alloc select state");

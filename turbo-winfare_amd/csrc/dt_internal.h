@@ -55,7 +55,7 @@ struct Head {
     uint32_t* mod_count = nullptr;     // [max_batch]
     uint32_t* block_start = nullptr;   // [max_batch][ntile + 1]
     void* list_scratch = nullptr;      // [max_batch][V] uint2 compaction lists (select)
-    unsigned long long* fv_part = nullptr;    // [kFvMaxBatch][kFvSlices][2][kFvBins]
+    unsigned long long* fv_acc = nullptr;     // [kFvMaxBatch][2][kFvBins], zero between steps
     unsigned long long* fv_merged = nullptr;  // [kFvMaxBatch][2][kFvBins]
     unsigned long long* fv_cand = nullptr;    // [kFvMaxBatch][kFvCandCap]
     void* fv_state = nullptr;                 // [kFvMaxBatch] x kFvStateBytes
@@ -171,8 +171,8 @@ struct SelectArgs {
     uint32_t* history;            // append target or null
     uint32_t hist_stride;
     uint32_t* hist_len;
-    // multi-workgroup full-vocabulary path (null fv_part: one workgroup per row)
-    unsigned long long* fv_part;    // [B][kFvSlices][2][kFvBins] slice histograms
+    // multi-workgroup full-vocabulary path (null fv_acc: one workgroup per row)
+    unsigned long long* fv_acc;     // [B][2][kFvBins] slice histograms summed by atomics
     unsigned long long* fv_merged;  // [B][2][kFvBins] merged histograms
     unsigned long long* fv_cand;    // [B][kFvCandCap] gathered candidates
     void* fv_state;                 // [B] x kFvStateBytes per-row plan and counters

@@ -810,10 +810,12 @@ __global__ __launch_bounds__(kMaxSelThreads) void k_fv_hist(SelectArgs a) {
     uint32_t beg, end;
     fv_slice(a.V, kFvSlices, k, &beg, &end);
     fv_hist(s, c, beg, end);
-    unsigned long long* dst = a.fv_part + ((size_t)b * kFvSlices + k) * 2u * kVBins;
+    // fixed-point bin weights are integers: summing the slices with atomics is exact and
+    // order-independent, and k_select reads one 32 KB histogram per row instead of 16
+    unsigned long long* acc = a.fv_acc + (size_t)b * 2u * kVBins;
     for (uint32_t i = threadIdx.x; i < kVBins; i += sel_nt()) {
-        dst[i] = s.vm[i];
-        dst[kVBins + i] = s.vq[i];
+        if (s.vm[i]) atomicAdd(&acc[i], s.vm[i]);
+        if (s.vq[i]) atomicAdd(&acc[kVBins + i], s.vq[i]);
     }
 }
 
@@ -970,7 +972,7 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
     for (uint32_t i = tid; i < kWinBins; i += NT) s.hu[i] = 0u;  // window histogram, below
 
     // the multi-workgroup hand-over is re-armed below only for rows this step defers
-    if (a.fv_part && tid == 0 && is_fv_row(row, a.V)) fv_state_of(a, b)->active = 0u;
+    if (a.fv_acc && tid == 0 && is_fv_row(row, a.V)) fv_state_of(a, b)->active = 0u;
 
     const bool sampled = row.temperature > 0.0f;
     // 1. row max, lowest argmax, finite minimum and, for sampled rows,
@@ -1290,17 +1292,16 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
         if (general) {
             const RowCtx c = make_ctx(a.V, lrow, m, fmin, row.temperature, scratch + (size_t)b * a.V);
             bool done = false;
-            if (want >= a.V && a.fv_part) {
-                // multi-workgroup rows: merge the slice histograms (exact integer sums), plan,
-                // and leave the gather and the draw to k_fv_gather and k_fv_finish
-                const unsigned long long* part = a.fv_part + (size_t)b * kFvSlices * 2u * kVBins;
+            if (want >= a.V && a.fv_acc) {
+                // multi-workgroup rows: take the summed slice histograms (and clear them for
+                // the next step), plan, and leave the gather and the draw to k_fv_gather and
+                // k_fv_finish
+                unsigned long long* acc = a.fv_acc + (size_t)b * 2u * kVBins;
                 unsigned long long* mg = a.fv_merged + (size_t)b * 2u * kVBins;
                 for (uint32_t i = tid; i < kVBins; i += sel_nt()) {
-                    unsigned long long hm = 0ull, hq = 0ull;
-                    for (uint32_t k = 0; k < kFvSlices; ++k) {
-                        hm += part[(size_t)k * 2u * kVBins + i];
-                        hq += part[(size_t)k * 2u * kVBins + kVBins + i];
-                    }
+                    const unsigned long long hm = acc[i], hq = acc[kVBins + i];
+                    acc[i] = 0ull;
+                    acc[kVBins + i] = 0ull;
                     s.vm[i] = hm;
                     s.vq[i] = hq;
                     mg[i] = hm;
@@ -1356,8 +1357,8 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
 
 void launch_select(const Head& h, int batch, const SelectArgs& args, bool any_fv, hipStream_t st) {
     SelectArgs a = args;
-    const bool multi = any_fv && (uint32_t)batch <= kFvMaxBatch && h.fv_part;
-    a.fv_part = multi ? h.fv_part : nullptr;
+    const bool multi = any_fv && (uint32_t)batch <= kFvMaxBatch && h.fv_acc;
+    a.fv_acc = multi ? h.fv_acc : nullptr;
     a.fv_merged = h.fv_merged;
     a.fv_cand = h.fv_cand;
     a.fv_state = h.fv_state;
