@@ -371,3 +371,29 @@ def test_back_to_back_steps_match_synchronised(head, batch, fv):
         h.step(inp, t)
         h.sync()
         assert np.array_equal(t.cpu().numpy(), async_toks[s]), s
+
+
+@pytest.mark.parametrize("kind", ["normal", "peaked"])
+def test_sampler_vocabulary_past_register_tiles(kind):
+    """A vocabulary of more than 4096 64-id blocks (here 300,000 ids): the select's row summary
+    loops over the block partials instead of holding them in registers, and the shortlist bound
+    comes from the histogram over the block maxima. Small D keeps the head cheap; the sampler
+    runs on caller logits."""
+    Vb, Db = 300000, 64
+    W, S, B, g = synth.make_head(Vb, Db, 31)
+    h = T.LMHead(W, S, B, g, vocab=Vb, hidden=Db)
+    try:
+        Bn = 6
+        base = (synth.normal(6, 81, Bn * Vb).reshape(Bn, Vb) * (4 if kind == "normal" else 24)).astype(np.float32)
+        cfgs = [(0.0, 1.0, 0, 0), (0.8, 0.95, 64, 0), (1.0, 0.9, 8, 0), (0.7, 1.0, 256, 0),
+                (1.0, 0.9, 0, 1), (0.6, 0.5, 0, 1)]
+        rows = [T.row_default(temperature=t, top_p=p, top_k=k, seed=19 + i, counter=2,
+                              flags=T.TURBO_ROW_FULL_VOCAB if f else 0)
+                for i, (t, p, k, f) in enumerate(cfgs)]
+        toks, after, rep = sample_given(h, base, rows)
+        assert np.array_equal(after, base)
+        check_sampler_on_gpu_logits(rows, toks, base, [T.row_uniform(r) for r in rows])
+        paths = rep.view(np.uint32)[:, 5]
+        assert paths[0] == 0 and all(paths[i] == 1 for i in (1, 2, 3)) and all(paths[i] == 2 for i in (4, 5))
+    finally:
+        h.close()

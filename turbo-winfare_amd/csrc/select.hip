@@ -81,8 +81,6 @@ struct SelShared {
     float wmin[kMaxSelWaves];
     float wzm[kMaxSelWaves];
     double wzs[kMaxSelWaves];
-    uint32_t gcnt[64];  // per 16-lane group (at most 64 groups)
-    uint32_t gtau[64];
     double bd[4];
     uint32_t bu[8];
 };
@@ -1090,7 +1088,7 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
             // ---- shortlist path ----
             // tau: a lower bound of the want-th largest block maximum, hence of the want-th
             // largest logit. With the keys in registers, a 256-bin window of width 1/32 below m
-            // (window_bound); else, or when the want-th maximum lies outside that window, one
+            // (window_add / window_scan); else, or when the want-th maximum lies outside it, one
             // histogram of the block maxima over 2048 bins of width 1/64 (the same bound over a
             // 32-unit span), and failing that the exact 22-bit key bound (two 11-bit levels).
             uint32_t tau = 0u;
