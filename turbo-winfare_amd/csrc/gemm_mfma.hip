@@ -19,7 +19,8 @@
 //    activations are stored k-permuted within each octet as (x0, x4, x1, x5, x2, x6, x3, x7)
 //    to match the order the dequant produces halves in.
 //  * Workgroup = 4 waves, one 64-row tile each, over a block of 32*NB batch columns
-//    (blockIdx.y: B = 256 runs two column blocks). Weights and activations are prefetched PF
+//    (B = 256 runs two column blocks, on the same XCD back to back so the second reads the
+//    weights from L2). Weights and activations are prefetched PF
 //    groups ahead into registers; the activations of group g+1 are written into the other half
 //    of a double-buffered LDS tile at the end of group g, one barrier per group.
 //  * Epilogue in place on the accumulators: per (column, 64-row tile), lane-local reductions
@@ -100,7 +101,7 @@ __device__ inline SbHalves unpack_sb(uint32_t sc) {
 __device__ inline uint32_t word_of(const uint4& w, int j) { return (j == 0) ? w.x : (j == 1) ? w.y : (j == 2) ? w.z : w.w; }
 
 // Workgroup = 4 waves, one 64-row tile each, over a block of NCOL = 32 NB batch columns
-// (blockIdx.y). Two or more independent workgroups share a CU, so one's epilogue overlaps
+// (the column block). Two or more independent workgroups share a CU, so one's epilogue overlaps
 // another's main loop and their barriers do not line up.
 // FULL: every column of the block exists (B % NCOL == 0): activation loads need no guard.
 // The main loop runs in rounds of PF groups (G % PF == 0) without branches: loads past the
@@ -110,7 +111,7 @@ __device__ inline uint32_t word_of(const uint4& w, int j) { return (j == 0) ? w.
 template <int NB, int PF, int OCC, bool FULL>
 __global__ __launch_bounds__(256, OCC) void k_head_mfma(
     const uint4* __restrict__ Wt, const uint32_t* __restrict__ SBt, const uint16_t* __restrict__ x16,
-    uint32_t B, uint32_t D, uint32_t NC, uint32_t G, EpiArgs ep) {
+    uint32_t B, uint32_t D, uint32_t NC, uint32_t G, uint32_t ncb, uint32_t ntg, EpiArgs ep) {
     constexpr uint32_t NT = 256;
     constexpr uint32_t NCOL = 32 * NB;
     constexpr uint32_t XP = NCOL * 8;                 // 16-byte activation pieces per group
@@ -119,8 +120,14 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
     __shared__ __attribute__((aligned(16))) _Float16 lx[2][NCOL * kColHalves];
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    const uint32_t cbase = blockIdx.y * NCOL;         // first batch column of this workgroup
-    const uint32_t tile_raw = blockIdx.x * 4u + wave;
+    // Workgroup i is dispatched to XCD i % 8. The ncb column blocks of one group of four tiles go
+    // to workgroups i, i + 8, ... of the same XCD, dispatched back to back, so every block after
+    // the first finds the tiles' weights in that XCD's L2 instead of reading HBM again.
+    const uint32_t wg = blockIdx.x, xcd = wg & 7u, slot = wg >> 3;
+    const uint32_t tg = (slot / ncb) * 8u + xcd;
+    if (tg >= ntg) return;                            // padding: ntg rounded up to 8
+    const uint32_t cbase = (slot % ncb) * NCOL;       // first batch column of this workgroup
+    const uint32_t tile_raw = tg * 4u + wave;
     const bool tile_ok = tile_raw < ep.ntile;
     const uint32_t tile = tile_ok ? tile_raw : ep.ntile - 1u;  // clamp loads; skip the epilogue
     const uint32_t hl = lane >> 5, l32 = lane & 31u;
@@ -373,12 +380,13 @@ void launch_head_mfma(const Head& h, int batch, const EpiArgs& ep, hipStream_t s
     if (B > 256u) throw std::runtime_error("MFMA head supports batch <= 256");
     const int nb = (B <= 32u) ? 1 : (B <= 64u) ? 2 : 4;
     const uint32_t ncol = 32u * (uint32_t)nb;
-    const dim3 grid((h.ntile + 3u) / 4u, (B + ncol - 1u) / ncol);
+    const uint32_t ntg = (h.ntile + 3u) / 4u, ncb = (B + ncol - 1u) / ncol;
+    const dim3 grid(ncb * ((ntg + 7u) / 8u) * 8u);
     const bool full = (B % ncol) == 0u;
     const bool pf2 = (h.G % 2u) == 0u;
 #define TDT_LAUNCH(NB, PF, OCC, FULL)                                                              \
     hipExtLaunchKernelGGL((k_head_mfma<NB, PF, OCC, FULL>), grid, dim3(256), 0, st, ev0, ev1, 0, h.Wt, \
-                          h.SBt, h.x16, B, h.D, h.NC, h.G, ep)
+                          h.SBt, h.x16, B, h.D, h.NC, h.G, ncb, ntg, ep)
 #define TDT_PICK(NB, OCC)                                                    \
     do {                                                                     \
         if (pf2) { if (full) TDT_LAUNCH(NB, 2, OCC, true); else TDT_LAUNCH(NB, 2, OCC, false); } \
