@@ -314,6 +314,67 @@ def test_digit_path_modifiers_bit_exact(head):
     check_sampler_on_gpu_logits(rows, toks, logits, [T.row_uniform(r) for r in rows])
 
 
+@pytest.mark.parametrize("dtype,normed", [("f32", False), ("bf16", False), ("f32", True)])
+def test_folded_step_matches_prepared_step(head, dtype, normed):
+    """Batches of one or two rows fold the RMSNorm, the digit planes and the history counts into
+    the head kernel (every workgroup recomputes them in LDS). A history stride past the folding
+    limit sends the same step through the preparation kernel instead: logits, tokens and the
+    appended history must agree bit for bit, and the folded modifiers must equal the oracle's
+    applied to the raw logits. The histories put ids on workgroup boundaries (multiples of 1024,
+    the last id), repeat ids and include ids past the vocabulary, which are ignored."""
+    h, _ = head
+    Bn = 2
+    x32 = synth.hidden_states(Bn, D, SEED + 31)
+    if normed:
+        xn = torch.empty((Bn, D), dtype=torch.float32, device="cuda")
+        h.rms_norm(dev(x32), Bn, xn)
+        h.sync()
+        x32 = xn.cpu().numpy()
+    if dtype == "bf16":
+        xin = dev(synth.f32_to_bf16(x32).view(np.int16))
+        hd = T.TURBO_HIDDEN_BF16
+    else:
+        xin = dev(x32)
+        hd = T.TURBO_HIDDEN_F32
+    rows = [T.row_default(temperature=0.9, top_k=40, top_p=0.9, repetition_penalty=1.3,
+                          presence_penalty=0.7, frequency_penalty=0.35, seed=5 + b, counter=3)
+            for b in range(Bn)]
+    n = 900
+    edge = np.array([0, 1023, 1024, 2047, 2048, 65535, 65536, V - 1, V, V + 7, 1024, 1024, V - 1],
+                    np.uint32)
+    hists = np.stack([np.concatenate([edge, synth.zipf_ids(n - edge.size, V, 1.1, SEED + 40 + b)])
+                      for b in range(Bn)]).astype(np.uint32)
+    lens = [n, n - 100]
+    flags = T.TURBO_STEP_APPEND_HISTORY | (T.TURBO_STEP_NORMED if normed else 0)
+    out = {}
+    for stride in (1024, 4096 + 64):  # folded, then through the preparation kernel
+        hb = np.zeros((Bn, stride), np.uint32)
+        hb[:, :n] = hists
+        hist = dev(hb.view(np.int32))
+        hl = torch.tensor(lens, dtype=torch.int32, device="cuda")
+        toks, logits = run_step(h, Bn, rows, xin, dtype=hd, flags=flags, history=hist, history_len=hl)
+        out[stride] = (toks, logits, hist.cpu().numpy().view(np.uint32), hl.cpu().numpy())
+    (t0, l0, h0, n0), (t1, l1, h1, n1) = out.values()
+    assert np.array_equal(l0.view(np.uint32), l1.view(np.uint32))
+    assert np.array_equal(t0, t1) and np.array_equal(n0, n1)
+    for b in range(Bn):
+        assert n0[b] == lens[b] + 1 and h0[b, lens[b]] == t0[b]
+        assert np.array_equal(h0[b, :lens[b] + 1], h1[b, :lens[b] + 1])
+    if dtype == "f32":
+        xn = dev(x32) if normed else torch.empty((Bn, D), dtype=torch.float32, device="cuda")
+        if not normed:
+            h.rms_norm(dev(x32), Bn, xn)
+        raw = torch.empty((Bn, V), dtype=torch.float32, device="cuda")
+        h.logits(xn, Bn, raw)
+        h.sync()
+        raw = raw.cpu().numpy()
+        for b in range(Bn):
+            want = O.apply_modifiers(raw[b], oparams(rows[b]), 30.0, history=hists[b, :lens[b]])
+            bad = np.nonzero(l0[b].view(np.uint32) != want.view(np.uint32))[0]
+            assert bad.size == 0, (b, int(bad.size), [(int(i), float(l0[b, i]), float(want[i])) for i in bad[:6]])
+    check_sampler_on_gpu_logits(rows, t0, l0, [T.row_uniform(r) for r in rows])
+
+
 def test_full_vocab_rows_split_over_workgroups(head):
     """Small batches split each full-vocabulary row over several workgroups (histogram and
     gather per slice, the last workgroup draws). Two calls in a row move a degenerate row (every

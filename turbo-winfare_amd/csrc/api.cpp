@@ -278,7 +278,8 @@ tdt::EpiArgs epi_args(const Head& h, float* logits, bool softcap) {
     return ep;
 }
 
-void launch_head(HandleBox& bx, int B, const tdt::EpiArgs& ep) {
+// fused: the small-batch step with the preparation folded into the head kernel (or null).
+void launch_head(HandleBox& bx, int B, const tdt::EpiArgs& ep, const tdt::FusedPrep* fused = nullptr) {
     Head& h = bx.h;
     const bool timed = h.timing && (h.t_launch++ % h.t_stride) == 0u;
     if (timed && h.t_count >= Head::kTimerSlots) {
@@ -293,7 +294,8 @@ void launch_head(HandleBox& bx, int B, const tdt::EpiArgs& ep) {
     }
     hipEvent_t ev0 = timed ? h.t_start[h.t_count] : nullptr;
     hipEvent_t ev1 = timed ? h.t_stop[h.t_count] : nullptr;
-    if (B <= 2) tdt::launch_head_digits(h, B, ep, h.stream, ev0, ev1);
+    if (fused) tdt::launch_head_digits_fused(h, B, *fused, ep, h.stream, ev0, ev1);
+    else if (B <= 2) tdt::launch_head_digits(h, B, ep, h.stream, ev0, ev1);
     else tdt::launch_head_mfma(h, B, ep, h.stream, ev0, ev1);
     if (timed) ++h.t_count;
 }
@@ -342,8 +344,36 @@ int run_rows(HandleBox& bx, const TurboStepInputs* in, const TurboStepOutputs* o
     if (has_bias) P = tdt::modtable_sort_size(h, in->bias_stride);
     float* logits = given_logits ? given_logits : (out->logits ? out->logits : (all_greedy ? nullptr : h.logits));
 
+    // Batches of one or two rows over the LM head's shape fold the preparation into the head
+    // kernel, unless a bias table is needed (it is sorted by the preparation kernel), the
+    // history is long enough that every workgroup scanning it would cost more than one kernel,
+    // or the hidden rows are not 16-byte aligned (the fold reads them in 16-byte pieces).
+    const bool fold = hidden && B <= tdt::kFusedRows && !has_bias && h.D <= tdt::kFusedMaxD &&
+                      h.ntile >= 2048u && (reinterpret_cast<uintptr_t>(hidden) & 15u) == 0u &&
+                      (!has_hist || in->history_stride <= tdt::kFusedHistMax);
+    if (fold) {
+        tdt::FusedPrep fp{};
+        fp.hidden = hidden;
+        fp.dtype = in->hidden_dtype == TURBO_HIDDEN_BF16 ? 1 : 0;
+        fp.normed = (in->flags & TURBO_STEP_NORMED) ? 1 : 0;
+        fp.gamma = h.gamma;
+        fp.eps = h.eps;
+        if (any_mods) {
+            fp.history = in->history;
+            fp.hist_len = in->history_len;
+            fp.hist_stride = in->history_stride;
+        }
+        fp.rows_dst = h.rows;
+        for (int b = 0; b < B; ++b) fp.inl[b] = rows[b];
+        tdt::EpiArgs ep = epi_args(h, logits, true);
+        ep.no_sumexp = any_short ? 0u : 1u;
+        ep.ban = in->ban_bits;
+        ep.ban_stride = in->ban_stride;
+        launch_head(bx, B, ep, &fp);
+    }
+
     tdt::PrepArgs pa = prep_args(h, B);
-    const int pos = stage_rows(h, rows, B, &pa);
+    const int pos = fold ? -1 : stage_rows(h, rows, B, &pa);
     pa.hidden = hidden;
     pa.dtype = in->hidden_dtype == TURBO_HIDDEN_BF16 ? 1 : 0;
     pa.normed = (in->flags & TURBO_STEP_NORMED) ? 1 : 0;
@@ -361,14 +391,16 @@ int run_rows(HandleBox& bx, const TurboStepInputs* in, const TurboStepOutputs* o
         pa.bias_stride = in->bias_stride;
         pa.bias_count = in->bias_count;
     }
-    tdt::launch_step_prep(h, pa, any_mods, h.stream);
-    release_slot(h, pos);
-    tdt::EpiArgs ep = epi_args(h, logits, hidden != nullptr);
-    ep.no_sumexp = any_short ? 0u : 1u;  // greedy and full-vocabulary rows do not read them
-    ep.ban = in->ban_bits;
-    ep.ban_stride = in->ban_stride;
-    if (hidden) launch_head(bx, B, ep);
-    else tdt::launch_logits_epilogue(h, B, ep, h.stream);
+    if (!fold) {
+        tdt::launch_step_prep(h, pa, any_mods, h.stream);
+        release_slot(h, pos);
+        tdt::EpiArgs ep = epi_args(h, logits, hidden != nullptr);
+        ep.no_sumexp = any_short ? 0u : 1u;  // greedy and full-vocabulary rows do not read them
+        ep.ban = in->ban_bits;
+        ep.ban_stride = in->ban_stride;
+        if (hidden) launch_head(bx, B, ep);
+        else tdt::launch_logits_epilogue(h, B, ep, h.stream);
+    }
 
     tdt::SelectArgs sa{};
     sa.V = h.V;

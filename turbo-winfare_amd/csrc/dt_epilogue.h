@@ -60,6 +60,32 @@ __device__ inline ModEntry lookup_mods(uint32_t id, uint32_t b, uint32_t tile, u
     return m;
 }
 
+// After the modifiers: ban, padding ids, the logit store and the block partial.
+__device__ inline void finish_wave(float l, uint32_t b, uint32_t tile, uint32_t lane, const EpiArgs& ep) {
+#pragma clang fp contract(off)
+    const uint32_t id = tile * kTileRows + lane;
+    const bool valid = id < ep.V;
+    if (ep.ban && valid) {
+        const uint32_t w = ep.ban[(size_t)b * ep.ban_stride + (id >> 5)];
+        if ((w >> (id & 31u)) & 1u) l = -INFINITY;
+    }
+    if (!valid) l = -INFINITY;
+    if (ep.logits && valid) ep.logits[(size_t)b * ep.V + id] = l;
+    const float m = wave_max(l);
+    const uint32_t arg = wave_min_u(l == m ? id : 0xFFFFFFFFu);
+    float se = (m == -INFINITY || ep.no_sumexp) ? 0.0f : __expf(l - m);
+    if (!ep.no_sumexp) se = wave_sum(se);
+    const float mn = wave_min(l == -INFINITY ? INFINITY : l);
+    if (lane == 0) {
+        BlockPartial bp;
+        bp.max = m;
+        bp.arg = arg;
+        bp.sumexp = se;
+        bp.minf = mn;
+        ep.partials[(size_t)b * ep.ntile + tile] = bp;
+    }
+}
+
 // acc: the raw head value of id = tile*64 + lane for batch row b (wave-uniform b and tile).
 __device__ inline void epilogue_wave(float acc, uint32_t b, uint32_t tile, uint32_t lane,
                                      const EpiArgs& ep) {
@@ -80,25 +106,18 @@ __device__ inline void epilogue_wave(float acc, uint32_t b, uint32_t tile, uint3
         const ModEntry m = lookup_mods(id, b, tile, hw, row, ep);
         if (m.count || m.has_bias) l = apply_entry(l, m, row, ep.rep_limit);
     }
-    if (ep.ban && valid) {
-        const uint32_t w = ep.ban[(size_t)b * ep.ban_stride + (id >> 5)];
-        if ((w >> (id & 31u)) & 1u) l = -INFINITY;
-    }
-    if (!valid) l = -INFINITY;
-    if (ep.logits && valid) ep.logits[(size_t)b * ep.V + id] = l;
-    const float m = wave_max(l);
-    const uint32_t arg = wave_min_u(l == m ? id : 0xFFFFFFFFu);
-    float se = (m == -INFINITY || ep.no_sumexp) ? 0.0f : __expf(l - m);
-    if (!ep.no_sumexp) se = wave_sum(se);
-    const float mn = wave_min(l == -INFINITY ? INFINITY : l);
-    if (lane == 0) {
-        BlockPartial bp;
-        bp.max = m;
-        bp.arg = arg;
-        bp.sumexp = se;
-        bp.minf = mn;
-        ep.partials[(size_t)b * ep.ntile + tile] = bp;
-    }
+    finish_wave(l, b, tile, lane, ep);
+}
+
+// The same with the id's history count given (no bias table): the folded small-batch step.
+__device__ inline void epilogue_wave_counted(float acc, uint32_t b, uint32_t tile, uint32_t lane,
+                                             const EpiArgs& ep, const DevRow& row, uint32_t count) {
+#pragma clang fp contract(off)
+    const uint32_t id = tile * kTileRows + lane;
+    float l = acc;
+    if (ep.cap > 0.0f) l = ep.cap * tanhf(l / ep.cap);
+    if (count && id < ep.V) l = apply_entry(l, ModEntry{id, count, 0.0f, 0u}, row, ep.rep_limit);
+    finish_wave(l, b, tile, lane, ep);
 }
 
 }  // namespace tdt

@@ -48,7 +48,7 @@ struct Head {
     DevRow* rows = nullptr;      // [max_batch]
     ModEntry* mods = nullptr;    // [max_batch][mod_cap] bias table sorted by id
     // History occurrence counts, zero between steps: the step prep adds, the head epilogue
-    // reads, the select kernel clears exactly the entries the step set.
+    // reads them and zeroes each entry it read.
     uint32_t* hcount = nullptr;  // [max_batch][V]
     uint32_t* hbits = nullptr;   // [max_batch][hbw] bit per id with a nonzero count
     uint32_t hbw = 0;            // ceil(V / 32)
@@ -147,6 +147,28 @@ void launch_repack(const Head& h, const uint8_t* W, const uint16_t* S, const uin
                    hipStream_t st);
 void launch_step_prep(const Head& h, const PrepArgs& a, bool with_mods, hipStream_t st);
 uint32_t modtable_sort_size(const Head& h, uint32_t n);
+
+// gemv_digits.hip: the small-batch step with the preparation folded into the head kernel.
+// Every workgroup recomputes the final RMSNorm and the digit planes of the whole row in LDS and
+// counts the history occurrences of its own ids there, so the step needs no preparation kernel
+// (and no hcount / hbits traffic). Bias tables still go through the preparation kernel.
+constexpr int kFusedRows = 2;
+constexpr uint32_t kFusedMaxD = 8192;       // digit planes of a row in LDS: D / 32 * 24 words
+constexpr uint32_t kFusedHistMax = 4096;    // history stride scanned by every workgroup
+struct FusedPrep {
+    const void* hidden;
+    int dtype;                   // 0 fp32, 1 bf16
+    int normed;
+    const uint16_t* gamma;
+    float eps;
+    const uint32_t* history;     // [B][hist_stride] or null
+    const uint32_t* hist_len;
+    uint32_t hist_stride;
+    DevRow* rows_dst;            // device row buffer for the select kernel (block 0 writes it)
+    DevRow inl[kFusedRows];
+};
+void launch_head_digits_fused(const Head& h, int batch, const FusedPrep& fp, const EpiArgs& ep,
+                              hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
 
 // gemv_digits.hip / gemm_mfma.hip
 // ev0 / ev1 (may be null): timing events stamped by the head kernel's own dispatch

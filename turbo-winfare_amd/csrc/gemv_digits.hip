@@ -18,6 +18,7 @@
 #include <hip/hip_ext.h>
 
 #include <algorithm>
+#include <stdexcept>
 
 #include "dt_epilogue.h"
 
@@ -112,6 +113,296 @@ __global__ __launch_bounds__(kDigitWaves * 64) void k_head_digits(
     }
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) epilogue_wave(acc[nb], (uint32_t)nb, tile, lane, ep);
+}
+
+// ---- the small-batch step with the preparation folded in ------------------------------------
+// One workgroup of 16 waves (one per CU) covers 16 consecutive tiles. Before streaming, each
+// workgroup recomputes what the step-prep kernel would have written, keeping it in LDS:
+//   * final RMSNorm (src/cpu_reference.cpp:43-52): double sum of squares, float mean + eps,
+//     1 / sqrt, each correctly rounded;
+//   * the block floating-point form of every 64-element group and its six digit planes: thread
+//     t owns octet t (elements 8t .. 8t + 7), so a group is 8 lanes (three DPP steps for its
+//     maximum and sum) and a lane writes its own digit words, the balanced base-16 digits of
+//     X read off Y = X + 0x888888 (its nibbles minus 8);
+//   * the occurrence count of each of its own 1024 ids in the row's history
+//     (src/sampling.cpp:81-89 visits every occurrence; ids past the vocabulary are ignored).
+// The loads of the row, its norm weight and its history are issued first, then the weight
+// prefetch, so this work runs while the first groups are in flight; it replaces a kernel launch
+// and its dependent-launch gap. Workgroup 0 also copies the row parameters to device memory for
+// the select kernel, after its stream.
+// The sum of squares adds in a different order from the step-prep kernel; the mean is rounded
+// to float from double either way, so the two agree except at a rounding tie of that float.
+constexpr uint32_t kFusedWaves = 16;
+constexpr uint32_t kFusedThreads = kFusedWaves * 64;
+constexpr uint32_t kFusedHistPer = kFusedHistMax / kFusedThreads;
+static_assert(kFusedMaxD == 8u * kFusedThreads, "one octet per thread");
+
+template <int NB>
+struct FusedLds {
+    uint32_t dig[NB][kFusedMaxD / 32 * kDigitWordsPerChunk];
+    float ws[NB][kFusedMaxD / 64];
+    float sum[NB][kFusedMaxD / 64];
+    uint32_t cnt[NB][kFusedThreads];  // history occurrences of the workgroup's ids
+    double red[NB][kFusedWaves];
+};
+
+// What the preparation reads, loaded before the weight stream is issued (loads complete in
+// order, so waiting for these does not wait for the stream).
+template <int NB>
+struct FusedIn {
+    uint4 x[NB][2];  // the thread's octet: fp32 in both, or bf16 pairs in the first
+    uint4 gw;        // the octet's bf16 norm weights
+    uint32_t hlen[NB];
+    uint32_t hid[NB][kFusedHistPer];
+};
+
+// Whether row nb's history is counted.
+__device__ inline bool fused_hist_on(const FusedPrep& fp, int nb) {
+    return fp.history != nullptr && (fp.inl[nb].has_mods & 1u) != 0u;
+}
+
+template <int NB>
+__device__ inline void fused_load(const FusedPrep& fp, uint32_t D, FusedIn<NB>& in) {
+    // Every load is unconditional, from an address that is always valid (the octet clamped to the
+    // row; an absent input reads the hidden row instead and is ignored), and nothing is done with
+    // the loaded bits here: a select or branch on a loaded value would make the wave wait for it.
+    const uint32_t tid = threadIdx.x;
+    const uint32_t o = min(tid, D / 8u - 1u);
+    const uint32_t esz = (fp.dtype == 1) ? 2u : 4u;
+    const char* xb = reinterpret_cast<const char*>(fp.hidden);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        const size_t off = (size_t)esz * ((size_t)nb * D + 8u * o);
+        in.x[nb][0] = *reinterpret_cast<const uint4*>(xb + off);
+        in.x[nb][1] = *reinterpret_cast<const uint4*>(xb + off + (esz == 4u ? 16u : 0u));
+    }
+    in.gw = fp.gamma ? reinterpret_cast<const uint4*>(fp.gamma)[o] : *reinterpret_cast<const uint4*>(xb);
+    const uint32_t* xw = reinterpret_cast<const uint32_t*>(fp.hidden);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        const bool on = fused_hist_on(fp, nb);
+        const uint32_t* h = on ? fp.history + (size_t)nb * fp.hist_stride : xw;
+        const uint32_t lim = on ? fp.hist_stride - 1u : 0u;
+        in.hlen[nb] = *(on ? fp.hist_len + nb : xw);
+#pragma unroll
+        for (uint32_t q = 0; q < kFusedHistPer; ++q) in.hid[nb][q] = h[min(tid + q * kFusedThreads, lim)];
+    }
+}
+
+__device__ inline uint32_t word_at(const uint4& v, int i) {
+    return (i == 0) ? v.x : (i == 1) ? v.y : (i == 2) ? v.z : v.w;
+}
+
+// value of 8-lane group reduction (lanes 8k .. 8k + 7)
+template <class T, class Op>
+__device__ inline T octet_group_reduce(T v, Op op) {
+    v = op(v, dpp_mov<dpp::kXor1>(v));
+    v = op(v, dpp_mov<dpp::kXor2>(v));
+    v = op(v, dpp_mov<dpp::kHalfMirror>(v));
+    return v;
+}
+
+template <int NB>
+__device__ void fused_prep(const FusedPrep& fp, uint32_t D, uint32_t V, const FusedIn<NB>& in, FusedLds<NB>& s) {
+#pragma clang fp contract(off)
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t idbase = blockIdx.x * kFusedThreads;
+    const bool ov = 8u * tid < D;  // this thread's octet lies in the row
+    // the octet's elements (0 past the row)
+    auto elems = [&](int nb, float (&v)[8]) {
+        if (fp.dtype == 1) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t w = word_at(in.x[nb][0], i);
+                v[2 * i] = bf16_to_f32(w & 0xFFFFu);
+                v[2 * i + 1] = bf16_to_f32(w >> 16);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(word_at(in.x[nb][i >> 2], i & 3));
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = ov ? v[i] : 0.0f;
+    };
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        s.cnt[nb][tid] = 0u;
+        if (!fp.normed) {
+            float v[8];
+            elems(nb, v);
+            double acc = 0.0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc += (double)v[i] * (double)v[i];
+            acc = wave_sum_d(acc);
+            if (lane == 0) s.red[nb][wave] = acc;
+        }
+    }
+    __syncthreads();  // partial sums written; counts zeroed
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        const uint32_t nh = fused_hist_on(fp, nb) ? min(in.hlen[nb], fp.hist_stride) : 0u;
+#pragma unroll
+        for (uint32_t q = 0; q < kFusedHistPer; ++q) {
+            const uint32_t i = tid + q * kFusedThreads, id = in.hid[nb][q];
+            if (i < nh && id < V && id - idbase < kFusedThreads) atomicAdd(&s.cnt[nb][id - idbase], 1u);
+        }
+    }
+    const uint32_t g = tid >> 3, j8 = tid & 7u;  // group and octet within it
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        if (8u * 64u * wave >= D) break;  // wave-uniform: no octet of this wave lies in the row
+        float v[8];
+        elems(nb, v);
+        if (!fp.normed) {
+            const double tot = wave_sum_d(lane < kFusedWaves ? s.red[nb][lane] : 0.0);
+            const float ms = (float)(tot / (double)D);
+            // sqrtf and 1.0f / s, each correctly rounded: computed in double and rounded once
+            const float sq = (float)sqrt((double)(ms + fp.eps));
+            const float inv = (float)(1.0 / (double)sq);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                v[i] = v[i] * inv;
+                if (fp.gamma) {
+                    const uint32_t w = word_at(in.gw, i >> 1);
+                    v[i] = v[i] * bf16_to_f32((i & 1) ? (w >> 16) : (w & 0xFFFFu));
+                }
+            }
+        }
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
+        m = octet_group_reduce(m, [](float a, float b) { return fmaxf(a, b); });
+        int e = 0;
+        (void)frexpf(m, &e);  // m = f * 2^e, f in [0.5, 1); e = 0 for m = 0
+        int X[8], sX = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            X[i] = (int)rintf(ldexpf(v[i], 21 - e));
+            sX += X[i];
+        }
+        sX = octet_group_reduce(sX, [](int a, int b) { return a + b; });
+        if (ov && j8 == 0u) {
+            s.ws[nb][g] = ldexpf(1.0f, e - 21);
+            s.sum[nb][g] = (float)sX * ldexpf(1.0f, e - 21);
+        }
+        uint32_t Z[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) Z[i] = ((uint32_t)X[i] + 0x888888u) ^ 0x888888u;
+        uint32_t* dst = &s.dig[nb][(2u * g + (j8 >> 2)) * kDigitWordsPerChunk + (j8 & 3u)];
+#pragma unroll
+        for (uint32_t k = 0; k < kDigits; ++k) {
+            uint32_t w = 0u;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) w |= ((Z[i] >> (4u * k)) & 15u) << (4u * i);
+            if (ov) dst[k * 4u] = w;
+        }
+    }
+    __syncthreads();  // digits, scales and counts complete
+}
+
+template <int NB>
+__global__ __launch_bounds__(kFusedThreads) void k_head_digits_fused(
+    const uint4* __restrict__ Wt, const uint32_t* __restrict__ SBt, uint32_t D, uint32_t NC, uint32_t G,
+    FusedPrep fp, EpiArgs ep) {
+    __shared__ __attribute__((aligned(16))) FusedLds<NB> s;
+    const uint32_t lane = threadIdx.x & 63u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t tile_raw = blockIdx.x * kFusedWaves + wave;
+    const bool tile_ok = tile_raw < ep.ntile;
+    const uint32_t tile = tile_ok ? tile_raw : ep.ntile - 1u;  // loads clamped; no epilogue
+    const uint4* wp = Wt + (size_t)tile * NC * kTileRows + lane;
+    const uint32_t* sbp = SBt + (size_t)tile * G * kTileRows + lane;
+
+    FusedIn<NB> in;
+    fused_load<NB>(fp, D, in);
+    __builtin_amdgcn_sched_barrier(0);  // keep the row's loads ahead of the weight stream
+    // branch-free (a group past the end is a repeated, unused load): with a branch here the
+    // compiler's wait for the row's loads would have to assume the shorter path and also wait
+    // for part of the stream
+    uint4 wa[kPF], wb[kPF];
+    uint32_t sb[kPF];
+#pragma unroll
+    for (int p = 0; p < kPF; ++p) {
+        const uint32_t gp = min((uint32_t)p, G - 1u);
+        wa[p] = load_stream(wp + (size_t)(2 * gp) * kTileRows);
+        wb[p] = load_stream(wp + (size_t)(2 * gp + 1) * kTileRows);
+        sb[p] = load_stream(sbp + (size_t)gp * kTileRows);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    fused_prep<NB>(fp, D, ep.V, in, s);
+
+    float acc[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[nb] = 0.0f;
+    for (uint32_t g0 = 0; g0 < G; g0 += kPF) {
+#pragma unroll
+        for (int p = 0; p < kPF; ++p) {
+            const uint32_t g = g0 + p;
+            if (g < G) {
+                const uint4 A = wa[p], Bw = wb[p];
+                const uint32_t sbw = sb[p];
+                const uint32_t gn = g + kPF;
+                if (gn < G) {
+                    wa[p] = load_stream(wp + (size_t)(2 * gn) * kTileRows);
+                    wb[p] = load_stream(wp + (size_t)(2 * gn + 1) * kTileRows);
+                    sb[p] = load_stream(sbp + (size_t)gn * kTileRows);
+                }
+                const uint32_t wq[8] = {A.x ^ 0x88888888u, A.y ^ 0x88888888u, A.z ^ 0x88888888u,
+                                        A.w ^ 0x88888888u, Bw.x ^ 0x88888888u, Bw.y ^ 0x88888888u,
+                                        Bw.z ^ 0x88888888u, Bw.w ^ 0x88888888u};
+                const float sf = bf16_to_f32(sbw & 0xFFFFu);
+                const float bf = bf16_to_f32(sbw >> 16);
+                const float c8 = fmaf(8.0f, sf, bf);
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) {
+                    const uint32_t* xd = &s.dig[nb][(2u * g) * kDigitWordsPerChunk];
+                    int a[kDigits];
+#pragma unroll
+                    for (uint32_t k = 0; k < kDigits; ++k) a[k] = 0;
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                            for (uint32_t k = 0; k < kDigits; ++k)
+                                a[k] = __builtin_amdgcn_sdot8((int)wq[4 * h + i],
+                                                              (int)xd[h * kDigitWordsPerChunk + k * 4 + i],
+                                                              a[k], false);
+                        }
+                    }
+                    uint32_t Dg = (uint32_t)a[0];
+#pragma unroll
+                    for (uint32_t k = 1; k < kDigits; ++k) Dg += (uint32_t)a[k] << (4u * k);
+                    const float t = sf * s.ws[nb][g];
+                    acc[nb] = fmaf((float)(int)Dg, t, acc[nb]);
+                    acc[nb] = fmaf(c8, s.sum[nb][g], acc[nb]);
+                }
+            }
+        }
+    }
+    // the row parameters for the select kernel (after the stream: this wait is free here)
+    if (blockIdx.x == 0u && threadIdx.x < NB * (sizeof(DevRow) / 4))
+        reinterpret_cast<uint32_t*>(fp.rows_dst)[threadIdx.x] = reinterpret_cast<const uint32_t*>(&fp.inl[0])[threadIdx.x];
+    if (!tile_ok) return;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        const uint32_t cnt = (fp.inl[nb].has_mods & 1u) ? s.cnt[nb][wave * 64u + lane] : 0u;
+        epilogue_wave_counted(acc[nb], (uint32_t)nb, tile, lane, ep, fp.inl[nb], cnt);
+    }
+}
+
+void launch_head_digits_fused(const Head& h, int batch, const FusedPrep& fp, const EpiArgs& ep,
+                              hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+    if (h.D > kFusedMaxD || h.D % kGroup != 0u) throw std::runtime_error("folded step needs D <= 8192");
+    const dim3 grid((h.ntile + kFusedWaves - 1u) / kFusedWaves), block(kFusedThreads);
+    if (batch == 1)
+        hipExtLaunchKernelGGL(k_head_digits_fused<1>, grid, block, 0, st, ev0, ev1, 0, h.Wt, h.SBt, h.D, h.NC,
+                              h.G, fp, ep);
+    else if (batch == 2)
+        hipExtLaunchKernelGGL(k_head_digits_fused<2>, grid, block, 0, st, ev0, ev1, 0, h.Wt, h.SBt, h.D, h.NC,
+                              h.G, fp, ep);
+    else
+        throw std::runtime_error("folded step supports batch 1 or 2");
+    check_hip(hipGetLastError(), "head (digit GEMV, folded preparation)");
 }
 
 // Matrices with few 64-row tiles (the projection shapes) give one wave per tile too little
