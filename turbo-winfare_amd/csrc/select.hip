@@ -83,6 +83,8 @@ struct SelShared {
     double wzs[kMaxSelWaves];
     double bd[4];
     uint32_t bu[8];
+    uint32_t ntile_q;   // shortlist: qualifying tiles appended (zeroed at kernel start)
+    uint32_t ncand_q;   // shortlist: gathered candidates appended (zeroed at kernel start)
 };
 
 // ---- block primitives ------------------------------------------------------------------------
@@ -181,7 +183,7 @@ __device__ inline int hist_cross(SelShared& s, uint32_t nb, T target, uint32_t* 
 }
 
 // Sorts s.cand[0, n) ascending with the bitonic network (n padded to a power of two).
-__device__ inline void sort_cand(SelShared& s, uint32_t n) {
+__device__ __attribute__((always_inline)) inline void sort_cand(SelShared& s, uint32_t n) {
     const uint32_t tid = threadIdx.x;
     uint32_t P = 2;
     while (P < n) P <<= 1;
@@ -225,7 +227,7 @@ __device__ inline uint32_t group_sum(uint32_t v, uint32_t P) {
 // Places the W smallest of the n (at most one per thread) distinct keys s.cand[0, n) in ascending order
 // at s.cand[0, W). Each key's rank is counted by a group of P threads (P as large as the block
 // allows), each over every P-th key, and summed across the group.
-__device__ void rank_top(SelShared& s, uint32_t n, uint32_t W) {
+__device__ __attribute__((always_inline)) inline void rank_top(SelShared& s, uint32_t n, uint32_t W) {
     const uint32_t tid = threadIdx.x;
     uint32_t lg = 0;
     while (lg < 6u && (n << (lg + 1u)) <= sel_nt()) ++lg;
@@ -499,7 +501,7 @@ __device__ __attribute__((always_inline)) inline void fv_hist(SelShared& s, cons
 }
 
 // From complete histograms in s.vm / s.vq: the nucleus bin and the draw range.
-__device__ void fv_plan(SelShared& s, const RowCtx& c, float top_p, float u, FvPlan* P) {
+__device__ __attribute__((always_inline)) inline void fv_plan(SelShared& s, const RowCtx& c, float top_p, float u, FvPlan* P) {
     const unsigned long long* hq = same_weights(c) ? s.vm : s.vq;
     uint32_t bb;
     // nucleus bin: where the T = 1 weight reaches top_p of the row total
@@ -893,7 +895,11 @@ __global__ __launch_bounds__(kMaxSelThreads) void k_fv_finish(SelectArgs a, uint
             rep.path = 2;
         } else {
             const DevRow row = a.rows[b];
-            radix_select(s, c, row, st->u, st->want, st->Z, st->arg, &token, &rep);
+            RowReport rr = rep;
+            uint32_t tk = token;
+            radix_select(s, c, row, st->u, st->want, st->Z, st->arg, &tk, &rr);
+            rep = rr;
+            token = tk;
         }
     }
     write_row(a, b, token, rep);
@@ -968,6 +974,7 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
     // history length for the append in write_row (thread 0), fetched now
     const uint32_t hlen = (tid == 0 && a.history && a.hist_len) ? a.hist_len[b] : 0u;
     for (uint32_t i = tid; i < kWinBins; i += NT) s.hu[i] = 0u;  // window histogram, below
+    if (tid == 0) { s.ntile_q = 0u; s.ncand_q = 0u; }
 
     // the multi-workgroup hand-over is re-armed below only for rows this step defers
     if (a.fv_acc && tid == 0 && is_fv_row(row, a.V)) fv_state_of(a, b)->active = 0u;
@@ -981,6 +988,10 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
     float m, fmin;
     uint32_t arg;
     double Z = 0.0;
+    // Shortlist rows with the window bound need Z only for the nucleus: their per-thread shares
+    // (zt) are summed while the gather's loads are in flight instead of before the bound.
+    double zt = 0.0;
+    bool late_z = false;
     if (reg) {
 #pragma unroll
         for (uint32_t j = 0; j < KP; ++j) key[j] = (tid + j * NT < a.ntile) ? float_key(p[j].max) : 0u;
@@ -1002,18 +1013,20 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
         if (lane < sel_nw()) { m = s.wmax[lane]; arg = s.warg[lane]; fmin = s.wmin[lane]; }
         wave_argmax(m, arg);
         fmin = wave_min(fmin);
+        late_z = win && fabsf(m) <= 1024.0f;
+        if (late_z) window_add<KP>(s, key, m);
         if (sampled && m != -INFINITY) {
-            double z = 0.0;
 #pragma unroll
             for (uint32_t j = 0; j < KP; ++j)
                 if (p[j].max != -INFINITY)
-                    z += (double)(__builtin_amdgcn_exp2f((p[j].max - m) * kLog2e) * p[j].sumexp);
-            z = wave_sum_d(z);
-            if (lane == 0) s.wzs[wave] = z;
+                    zt += (double)(__builtin_amdgcn_exp2f((p[j].max - m) * kLog2e) * p[j].sumexp);
+            if (!late_z) {
+                const double z = wave_sum_d(zt);
+                if (lane == 0) s.wzs[wave] = z;
+            }
         }
-        if (win && fabsf(m) <= 1024.0f) window_add<KP>(s, key, m);
         __syncthreads();
-        if (sampled && m != -INFINITY) Z = wave_sum_d(lane < sel_nw() ? s.wzs[lane] : 0.0);
+        if (!late_z && sampled && m != -INFINITY) Z = wave_sum_d(lane < sel_nw() ? s.wzs[lane] : 0.0);
     } else {
         // any number of tiles: a loop over the partials with a running maximum for Z; the
         // block-maximum keys are kept in LDS when they fit
@@ -1080,7 +1093,20 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
         // Full-vocabulary rows take Z from their value histogram (the head may skip the block
         // sums of exp when no row needs them): a finite maximum is the only condition.
         const bool fvrow = want >= a.V;
-        if (m == -INFINITY || (!fvrow && !(Z > 0.0))) {
+        // the deferred Z: wave shares (stage 1, before a barrier), then every wave adds them
+        auto z_stage1 = [&]() {
+            const double z = wave_sum_d(zt);
+            if (lane == 0) s.wzs[wave] = z;
+        };
+        auto z_stage2 = [&]() {
+            Z = wave_sum_d(lane < sel_nw() ? s.wzs[lane] : 0.0);
+            rep.total = Z;
+            late_z = false;
+        };
+        // with m finite, the tile holding m contributes at least exp(0) to Z (its block sum
+        // is computed whenever a row samples from a shortlist): the deferred check below only
+        // catches non-finite sums
+        if (m == -INFINITY || (!fvrow && !late_z && !(Z > 0.0))) {
             token = 0xFFFFFFFFu;
             rep.path = 3;
             general = false;
@@ -1138,18 +1164,13 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
             // tiles whose maximum reaches tau, compacted into s.tiles
             uint32_t nq = 0u;
             if (reg) {
-                uint32_t hm = 0u;
+                // one LDS atomic per wave and key slot; the tile order does not matter (the
+                // candidates are ranked by value and id)
 #pragma unroll
                 for (uint32_t j = 0; j < KP; ++j)
-                    if (key[j] >= tau && key[j] != 0u) hm |= 1u << j;
-                uint32_t o = block_excl_scan<uint32_t>((uint32_t)__popc(hm), s, &nq);
-#pragma unroll
-                for (uint32_t j = 0; j < KP; ++j)
-                    if ((hm >> j) & 1u) {
-                        if (o < kTileCap) s.tiles[o] = tid + j * NT;
-                        ++o;
-                    }
+                    wave_append(&s.ntile_q, key[j] >= tau && key[j] != 0u, tid + j * NT, s.tiles, kTileCap);
                 __syncthreads();
+                nq = s.ntile_q;
             } else {
                 if (tid == 0) s.bu[3] = 0u;
                 __syncthreads();
@@ -1164,9 +1185,11 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
             }
             if (nq > kTileCap) {
                 general = true;
+                if (late_z) { z_stage1(); __syncthreads(); z_stage2(); }
             } else {
-                // gather the elements >= tau of those tiles: GB loads in flight per thread, a hit
-                // mask, one block scan for the output offsets per round
+                // gather the elements >= tau of those tiles: GB loads in flight per thread (issued
+                // unconditionally from clamped ids, so no branch separates them), appended with one
+                // LDS atomic per wave and slot
                 constexpr uint32_t GB = kGatherChunk / NT;
                 const uint32_t items = nq * kTileRows;
                 uint32_t n = 0u;
@@ -1176,27 +1199,24 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
 #pragma unroll
                     for (uint32_t q = 0; q < GB; ++q) {
                         const uint32_t it = c0 + q * NT + tid;
-                        id[q] = (it < items) ? s.tiles[it >> 6] * kTileRows + (it & 63u) : 0xFFFFFFFFu;
-                        v[q] = (id[q] < a.V) ? lrow[id[q]] : -INFINITY;
+                        id[q] = (it < items) ? s.tiles[min(it, items - 1u) >> 6] * kTileRows + (it & 63u) : 0xFFFFFFFFu;
+                        v[q] = lrow[min(id[q], a.V - 1u)];
                     }
-                    uint32_t hm = 0u;
+                    if (late_z && c0 == 0u) z_stage1();  // while the loads are in flight
 #pragma unroll
                     for (uint32_t q = 0; q < GB; ++q)
-                        if (id[q] < a.V && float_key(v[q]) >= tau) hm |= 1u << q;
-                    uint32_t tot = 0u;
-                    uint32_t o = n + block_excl_scan<uint32_t>((uint32_t)__popc(hm), s, &tot);
-#pragma unroll
-                    for (uint32_t q = 0; q < GB; ++q)
-                        if ((hm >> q) & 1u) {
-                            if (o < kCandCap) s.cand[o] = ((unsigned long long)(~float_key(v[q])) << 32) | id[q];
-                            ++o;
-                        }
-                    n += tot;
+                        wave_append(&s.ncand_q, id[q] < a.V && float_key(v[q]) >= tau,
+                                    ((unsigned long long)(~float_key(v[q])) << 32) | id[q], s.cand, kCandCap);
                 }
+                if (late_z && items == 0u) z_stage1();
                 __syncthreads();
+                n = s.ncand_q;
+                if (late_z) z_stage2();
                 if (n > kCandCap) general = true;
-                __syncthreads();
-                if (!general) {
+                if (!general && !(Z > 0.0)) {
+                    token = 0xFFFFFFFFu;  // a non-finite Z: the degenerate report, as above
+                    rep.path = 3;
+                } else if (!general) {
                     // counting ranks costs n^2 / threads compares per thread: the network beyond 256
                     if (n <= 256u) rank_top(s, n, min(want, n));
                     else sort_cand(s, n);
@@ -1346,7 +1366,15 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
                     done = true;
                 }
             }
-            if (!done) radix_select(s, c, row, u, want, Z, arg, &token, &rep);
+            if (!done) {
+                // the fallback writes through pointers: copies keep the kernel's own report and
+                // token out of addressable (scratch) memory on every other path
+                RowReport rr = rep;
+                uint32_t tk = token;
+                radix_select(s, c, row, u, want, Z, arg, &tk, &rr);
+                rep = rr;
+                token = tk;
+            }
         }
     }
 
