@@ -242,7 +242,8 @@ def main():
     head = T.LMHead(W, S, B, g, vocab=V, hidden=D)
     # Events around a launch add a few microseconds of gap, so the head kernel is timed on every
     # 16th step of the timed region (its average duration; the step rate is not perturbed).
-    head.enable_head_timing(True, every=16)
+    # Short runs (counter passes) time every launch so that at least one is timed.
+    head.enable_head_timing(True, every=16 if a.steps >= 64 else 1)
     if a.only in ("b32", "b256"):
         B = 32 if a.only == "b32" else 256
         res = batched_line(T, torch, head, B, a.warmup, a.steps)
