@@ -375,6 +375,54 @@ def test_folded_step_matches_prepared_step(head, dtype, normed):
     check_sampler_on_gpu_logits(rows, t0, l0, [T.row_uniform(r) for r in rows])
 
 
+def test_b1_back_to_back_steps_cover_every_tile(head):
+    """B = 1 steps (the folded head: every workgroup recomputes the row's norm, digits and the
+    history counts of its own ids) run back to back without a host sync, into NaN-filled
+    outputs, while each step appends its token to the history the next one counts. Every logit
+    must equal the prepared path's with the oracle's modifiers applied (to fp32 rounding of the
+    modifier arithmetic; a repetition penalty of 1.2 on a miscounted id would be far outside
+    it), and the tokens must be the oracle sampler's on those logits."""
+    h, _ = head
+    steps = 5
+    xs = [synth.hidden_states(1, D, SEED + 60, k) for k in range(steps)]
+    hist0 = synth.zipf_ids(300, V, 1.1, SEED + 61).astype(np.uint32)
+    hist0[:4] = [0, 63, 64, V - 1]
+    cap = 300 + steps
+    hist = torch.zeros((1, cap), dtype=torch.int32, device="cuda")
+    hist[0, :300] = torch.from_numpy(hist0.view(np.int32))
+    hlen = torch.tensor([300], dtype=torch.int32, device="cuda")
+    rows = [T.row_default(temperature=0.9, top_k=50, top_p=0.9, repetition_penalty=1.2,
+                          seed=SEED + 62, counter=k) for k in range(steps)]
+    outs = []
+    xd = [dev(x) for x in xs]  # kept alive: the inputs hold raw device pointers
+    for k in range(steps):
+        inp, keep = h.make_inputs(1, [rows[k]], hidden=xd[k], flags=T.TURBO_STEP_APPEND_HISTORY,
+                                  history=hist, history_len=hlen)
+        tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+        lg = torch.full((1, V), float("nan"), dtype=torch.float32, device="cuda")
+        h.step(inp, tok, lg)
+        outs.append((tok, lg, keep))
+    h.sync()
+    hist_h = hist.cpu().numpy().view(np.uint32)[0]
+    for k in range(steps):
+        tok, lg, _ = outs[k]
+        got = lg.cpu().numpy()[0]
+        assert not np.isnan(got).any(), (k, int(np.isnan(got).sum()))
+        xn = torch.empty((1, D), dtype=torch.float32, device="cuda")
+        h.rms_norm(dev(xs[k]), 1, xn)
+        raw = torch.empty((1, V), dtype=torch.float32, device="cuda")
+        h.logits(xn, 1, raw)
+        h.sync()
+        raw = raw.cpu().numpy()[0]
+        hk = hist_h[:300 + k]
+        want = O.apply_modifiers(raw, oparams(rows[k]), 30.0, history=hk)
+        scale = float(np.abs(raw).max())
+        assert np.allclose(got, want, rtol=1e-5, atol=1e-6 * scale), (k, float(np.abs(got - want).max()))
+        check_sampler_on_gpu_logits([rows[k]], tok.cpu().numpy().astype(np.uint32), got[None, :],
+                                    [T.row_uniform(rows[k])])
+        assert int(hist_h[300 + k]) == int(tok.item())
+
+
 def test_full_vocab_rows_split_over_workgroups(head):
     """Small batches split each full-vocabulary row over several workgroups (histogram and
     gather per slice, the last workgroup draws). Two calls in a row move a degenerate row (every
