@@ -19,6 +19,7 @@ struct BlockPartial {
     uint32_t arg;    // lowest id holding the maximum
     float sumexp;    // sum exp(l - max) over the block (0 when max is -inf)
     float minf;      // smallest finite logit of the block (+inf when none)
+    float smax;      // second-largest logit of the block, counting repeats (-inf when none)
 };
 
 // One sorted modifier entry (per row, unique id).

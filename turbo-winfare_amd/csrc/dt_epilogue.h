@@ -5,7 +5,8 @@
 //   repetition   per occurrence, clamp +-0.9999*softcap  src/sampling.cpp:74-90
 //   presence / frequency                                 (extension)
 //   ban          -> -inf                                 (extension)
-// then stores the logit (optional) and the block partial (max, lowest argmax, sum exp(l-max)).
+// then stores the logit (optional) and the block partial (max, lowest argmax, sum exp(l-max),
+// smallest finite value, second-largest value).
 // Floating-point contraction is off in these functions (the library is built with
 // -ffp-contract=fast-honor-pragmas): a fused multiply-add would round once where the reference
 // rounds twice, e.g. in l - frequency * count or in cap * tanh(z / cap) + bias.
@@ -73,6 +74,7 @@ __device__ inline void finish_wave(float l, uint32_t b, uint32_t tile, uint32_t 
     if (ep.logits && valid) ep.logits[(size_t)b * ep.V + id] = l;
     const float m = wave_max(l);
     const uint32_t arg = wave_min_u(l == m ? id : 0xFFFFFFFFu);
+    const float sm = wave_max(id == arg ? -INFINITY : l);  // a repeat of the maximum counts
     float se = (m == -INFINITY || ep.no_sumexp) ? 0.0f : __expf(l - m);
     if (!ep.no_sumexp) se = wave_sum(se);
     const float mn = wave_min(l == -INFINITY ? INFINITY : l);
@@ -82,6 +84,7 @@ __device__ inline void finish_wave(float l, uint32_t b, uint32_t tile, uint32_t 
         bp.arg = arg;
         bp.sumexp = se;
         bp.minf = mn;
+        bp.smax = sm;
         ep.partials[(size_t)b * ep.ntile + tile] = bp;
     }
 }

@@ -318,14 +318,20 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
                 for (int r = 0; r < 16; ++r)
                     if (base + 32u * mb + acc_row(r, hl) >= ep.V) acc[mb][nb][r] = -INFINITY;
         }
-        float bmax = -INFINITY, bmin = INFINITY;
+        float bmax = -INFINITY, bmin = INFINITY, bsec = -INFINITY;  // bsec: second largest, with repeats
         uint32_t barg = 0xFFFFFFFFu;
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const float z = acc[mb][nb][r];
-                if (z > bmax) { bmax = z; barg = base + 32u * mb + acc_row(r, hl); }  // rows in increasing order
+                if (z > bmax) {  // rows in increasing order
+                    bsec = bmax;
+                    bmax = z;
+                    barg = base + 32u * mb + acc_row(r, hl);
+                } else {
+                    bsec = fmaxf(bsec, z);
+                }
                 if (z != -INFINITY) bmin = fminf(bmin, z);
             }
         bmin = fminf(bmin, xor32(bmin));
@@ -349,6 +355,8 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
         }
         const float om = xor32(bmax);
         const uint32_t oa = xor32(barg);
+        // second largest of the two halves together: the smaller maximum or the larger second
+        bsec = fmaxf(fmaxf(bsec, xor32(bsec)), fminf(bmax, om));
         if (om > bmax || (om == bmax && oa < barg)) { bmax = om; barg = oa; }
         float se = 0.0f;
         if (bmax != -INFINITY && !ep.no_sumexp) {
@@ -366,6 +374,7 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
             bp.arg = (bmax == -INFINITY) ? base : barg;
             bp.sumexp = se;
             bp.minf = bmin;
+            bp.smax = bsec;
             ep.partials[(size_t)bq * ep.ntile + tile] = bp;
         }
     };

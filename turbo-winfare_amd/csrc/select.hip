@@ -970,7 +970,7 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
     for (uint32_t j = 0; j < KP; ++j) p[j] = parts[min(tid + j * NT, a.ntile - 1u)];
 #pragma unroll
     for (uint32_t j = 0; j < KP; ++j)
-        if (tid + j * NT >= a.ntile) p[j] = BlockPartial{-INFINITY, 0xFFFFFFFFu, 0.0f, INFINITY};
+        if (tid + j * NT >= a.ntile) p[j] = BlockPartial{-INFINITY, 0xFFFFFFFFu, 0.0f, INFINITY, -INFINITY};
     // history length for the append in write_row (thread 0), fetched now
     const uint32_t hlen = (tid == 0 && a.history && a.hist_len) ? a.hist_len[b] : 0u;
     for (uint32_t i = tid; i < kWinBins; i += NT) s.hu[i] = 0u;  // window histogram, below
@@ -1164,11 +1164,19 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
             // tiles whose maximum reaches tau, compacted into s.tiles
             uint32_t nq = 0u;
             if (reg) {
-                // one LDS atomic per wave and key slot; the tile order does not matter (the
-                // candidates are ranked by value and id)
+                // A qualifying tile whose second-largest value lies below tau holds exactly one
+                // element >= tau, its maximum, known from the partial: it is appended as a
+                // candidate directly. Only the other qualifying tiles are gathered. One LDS atomic
+                // per wave and key slot; the order does not matter (candidates are ranked by value
+                // and id).
 #pragma unroll
-                for (uint32_t j = 0; j < KP; ++j)
-                    wave_append(&s.ntile_q, key[j] >= tau && key[j] != 0u, tid + j * NT, s.tiles, kTileCap);
+                for (uint32_t j = 0; j < KP; ++j) {
+                    const bool qual = key[j] >= tau && key[j] != 0u;
+                    const bool one = qual && float_key(p[j].smax) < tau;
+                    wave_append(&s.ncand_q, one, ((unsigned long long)(~key[j]) << 32) | p[j].arg, s.cand, kCandCap);
+                    wave_append(&s.ntile_q, qual && !one, tid + j * NT, s.tiles, kTileCap);
+                }
+                if (late_z) z_stage1();
                 __syncthreads();
                 nq = s.ntile_q;
             } else {
@@ -1185,7 +1193,7 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
             }
             if (nq > kTileCap) {
                 general = true;
-                if (late_z) { z_stage1(); __syncthreads(); z_stage2(); }
+                if (late_z) z_stage2();  // its wave shares were written before the last barrier
             } else {
                 // gather the elements >= tau of those tiles: GB loads in flight per thread (issued
                 // unconditionally from clamped ids, so no branch separates them), appended with one
@@ -1202,14 +1210,12 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
                         id[q] = (it < items) ? s.tiles[min(it, items - 1u) >> 6] * kTileRows + (it & 63u) : 0xFFFFFFFFu;
                         v[q] = lrow[min(id[q], a.V - 1u)];
                     }
-                    if (late_z && c0 == 0u) z_stage1();  // while the loads are in flight
 #pragma unroll
                     for (uint32_t q = 0; q < GB; ++q)
                         wave_append(&s.ncand_q, id[q] < a.V && float_key(v[q]) >= tau,
                                     ((unsigned long long)(~float_key(v[q])) << 32) | id[q], s.cand, kCandCap);
                 }
-                if (late_z && items == 0u) z_stage1();
-                __syncthreads();
+                if (items > 0u) __syncthreads();  // else every append happened before the last barrier
                 n = s.ncand_q;
                 if (late_z) z_stage2();
                 if (n > kCandCap) general = true;
