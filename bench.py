@@ -285,7 +285,7 @@ def main():
                    "vocab": V, "hidden": D, "group": 64, "batch": 1, "softcap": 30.0},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-                     "kernel": "k_head_digits<1>", "kernel_avg_us": 1e3 * kavg_ms,
+                     "kernel": "k_head_digits_fused<1>", "kernel_avg_us": 1e3 * kavg_ms,
                      "algorithmic_bytes_per_launch": bytes_per_launch},
     }
     if not a.no_batches and a.only is None:
