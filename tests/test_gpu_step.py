@@ -155,6 +155,28 @@ def test_config4_b256_full_vocab_nucleus(head):
         assert U.logit_err(logits[b], want_l) <= U.LOGIT_RTOL
 
 
+def test_b256_logits_equal_b32_logits(head):
+    """At B = 256 the MFMA head stores its logits through an LDS transpose (four column blocks of
+    32 rows per workgroup); at B = 32 it stores them straight from the accumulators. Every
+    column's arithmetic is the same (same k order, same dequant, same epilogue), so the rows of a
+    256-row batch must equal, bit for bit, the same rows run as 32-row batches."""
+    h, _ = head
+    xb = synth.f32_to_bf16(synth.hidden_states(256, D, SEED + 13))
+    x = dev(xb.view(np.int16))
+    big = torch.empty((256, V), dtype=torch.float32, device="cuda")
+    h.logits(x, 256, big, dtype=T.TURBO_HIDDEN_BF16)
+    h.sync()
+    big = big.cpu().numpy()
+    for r0 in (0, 96, 224):
+        xs = dev(xb[r0:r0 + 32].view(np.int16))
+        small = torch.empty((32, V), dtype=torch.float32, device="cuda")
+        h.logits(xs, 32, small, dtype=T.TURBO_HIDDEN_BF16)
+        h.sync()
+        small = small.cpu().numpy()
+        bad = np.nonzero((big[r0:r0 + 32].view(np.uint32) != small.view(np.uint32)).any(axis=1))[0]
+        assert bad.size == 0, (r0, [int(r0 + i) for i in bad[:8]])
+
+
 def test_config5_constrained_b64(head):
     h, (W, S, B, g) = head
     Bn = 64

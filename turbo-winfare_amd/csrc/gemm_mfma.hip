@@ -243,6 +243,13 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
     if (!tile_ok) return;
 
     // ---- epilogue, in place on the accumulators ----
+    // The transposed logit stores reuse the activation buffer: one 32 x kTrRow float tile per
+    // wave (rows padded to spread the LDS banks), after every wave's last read of it (the main
+    // loop ends with a barrier).
+    constexpr uint32_t kTrRow = 68;
+    constexpr bool kTransposeStores = NB == 4;
+    static_assert(!kTransposeStores || sizeof(lx) >= 4u * 32u * kTrRow * sizeof(float),
+                  "four wave tiles must fit the activation buffer");
     const uint32_t base = tile * kTileRows;
     const bool vec_ok = (ep.V & 3u) == 0u;  // float4 stores need 16-byte aligned rows
     const bool full_tile = base + kTileRows <= ep.V;
@@ -335,7 +342,27 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
                 if (z != -INFINITY) bmin = fminf(bmin, z);
             }
         bmin = fminf(bmin, xor32(bmin));
-        if (col_ok && ep.logits) {
+        // Logits: with four column blocks (B = 256) the activation buffer is free after the main
+        // loop, and each wave transposes its 64 x 32 tile through its own 8.5 KiB of it, so that
+        // one float4 store covers four whole 256-byte row segments instead of 16 bytes of 32
+        // rows. Otherwise (and for partial tiles or columns) the values leave as they lie.
+        if (kTransposeStores && ep.logits && full_tile && vec_ok && cbase + 32u * nb + 32u <= B) {
+            float* tl = reinterpret_cast<float*>(&lx[0][0]) + wave * (32u * kTrRow);
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    *reinterpret_cast<float4*>(tl + l32 * kTrRow + 32u * mb + 8u * q + 4u * hl) =
+                        make_float4(acc[mb][nb][4 * q], acc[mb][nb][4 * q + 1], acc[mb][nb][4 * q + 2],
+                                    acc[mb][nb][4 * q + 3]);
+            const uint32_t c0 = lane >> 4, r4 = 4u * (lane & 15u);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t c = 4u * (uint32_t)i + c0;  // column of the tile
+                const float4 v = *reinterpret_cast<const float4*>(tl + c * kTrRow + r4);
+                *reinterpret_cast<float4*>(ep.logits + (size_t)(cbase + 32u * nb + c) * ep.V + base + r4) = v;
+            }
+        } else if (col_ok && ep.logits) {
             float* lrow = ep.logits + (size_t)bq * ep.V + base;
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb)
