@@ -397,6 +397,27 @@ def test_folded_step_matches_prepared_step(head, dtype, normed):
     check_sampler_on_gpu_logits(rows, t0, l0, [T.row_uniform(r) for r in rows])
 
 
+def test_unaligned_hidden_takes_the_prepared_path(head):
+    """The folded head reads the hidden row in 16-byte pieces, so a row that is not 16-byte
+    aligned goes through the preparation kernel instead: the same row at an aligned and at an
+    unaligned address must give the same logits and token (greedy and sampled with history)."""
+    h, _ = head
+    x = synth.hidden_states(1, D, SEED + 70)[0]
+    buf = torch.zeros(D + 4, dtype=torch.float32, device="cuda")
+    buf[1:D + 1] = torch.from_numpy(x).cuda()
+    un = buf[1:D + 1].view(1, D)                      # 4-byte offset
+    al = dev(x[None, :])
+    assert un.data_ptr() % 16 == 4 and al.data_ptr() % 16 == 0
+    hist = dev(synth.zipf_ids(200, V, 1.1, SEED + 71).astype(np.int32)[None, :])
+    hl = torch.tensor([200], dtype=torch.int32, device="cuda")
+    for r in (T.row_default(), T.row_default(temperature=0.8, top_k=64, top_p=0.95, repetition_penalty=1.1,
+                                             seed=SEED, counter=7)):
+        t1, l1 = run_step(h, 1, [r], al, history=hist, history_len=hl)
+        t2, l2 = run_step(h, 1, [r], un, history=hist, history_len=hl)
+        assert np.array_equal(l1.view(np.uint32), l2.view(np.uint32))
+        assert np.array_equal(t1, t2)
+
+
 def test_b1_back_to_back_steps_cover_every_tile(head):
     """B = 1 steps (the folded head: every workgroup recomputes the row's norm, digits and the
     history counts of its own ids) run back to back without a host sync, into NaN-filled
