@@ -55,7 +55,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-batches", action="store_true")
     ap.add_argument("--cpu-steps", type=int, default=4)
-    ap.add_argument("--only", choices=["b1", "b32", "b256"], default=None,
+    ap.add_argument("--only", choices=["b1", "b32", "b256", "widened"], default=None,
                     help="run one workload only (profiling); prints its own JSON line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="copy a buffer of the table's size 5 times (a plain copy kernel of known "
@@ -153,7 +153,9 @@ def widened_lines(T, torch):
     """Rows beyond the decode tail that share its kernels: the int4 matvec at the reference's
     projection shapes (B = 1; digit GEMV, split over the groups of each 64-row tile) and the
     embedding lookup on the tied table. Kernel times come from the head's dispatch events on
-    every call; call times are wall clock per call (prep + kernel launches included)."""
+    every call of a second loop (the events themselves lengthen a short kernel's measured
+    span); call times are wall clock per call of a loop without them (preparation and head
+    kernels, host launch cost included)."""
     import synth
     out = {"matvec_b1": {}, "embed": {}}
     for rows, k in [(704, 2816), (2816, 704), (2112, 2816), (2816, 2112), (4096, 2816)]:
@@ -239,6 +241,9 @@ def main():
     import turbo_decode_tail as T
 
     assert torch.cuda.is_available(), "bench needs a GPU"
+    if a.only == "widened":
+        print(json.dumps({"only": a.only, **widened_lines(T, torch)}), flush=True)
+        return
     log("generating the synthetic head")
     W, S, B, g = synth.make_head(V, D, SEED)
     head = T.LMHead(W, S, B, g, vocab=V, hidden=D)
