@@ -39,3 +39,65 @@ def test_matvec_projection_shapes(rows, in_dim):
                     assert float(err.max()) <= 2e-3, (batch, b, float(err.max()))
     finally:
         h.close()
+
+
+@pytest.mark.parametrize("rows,in_dim", SHAPES)
+@pytest.mark.parametrize("bf16", [False, True])
+def test_folded_matvec_matches_prepared(rows, in_dim, bf16):
+    """One or two 16-byte-aligned rows run the split kernel with the digit planes computed in
+    each workgroup (no preparation kernel); a row at a 4-byte offset takes the preparation
+    kernel. Both must give bit-identical outputs, for fp32 and bf16 input."""
+    W, S, B, _ = synth.make_head(rows, in_dim, rows + in_dim + 1)
+    h = T.LMHead(W, S, B, None, vocab=rows, hidden=in_dim, softcap=0.0)
+    try:
+        for batch in (1, 2):
+            x = synth.hidden_states(batch, in_dim, 60 + batch)
+            if bf16:
+                xs = torch.from_numpy(synth.f32_to_bf16(x).view(np.int16)).cuda()
+                dt = T.TURBO_HIDDEN_BF16
+                pad = 8  # 16 bytes of bf16: the unaligned copy starts 2 elements (4 bytes) in
+            else:
+                xs = torch.from_numpy(x).cuda()
+                dt = T.TURBO_HIDDEN_F32
+                pad = 4
+            flat = xs.reshape(-1)
+            buf = torch.zeros(flat.numel() + pad, dtype=flat.dtype, device="cuda")
+            off = 2 if bf16 else 1
+            buf[off:off + flat.numel()] = flat
+            un = buf[off:off + flat.numel()]
+            assert xs.data_ptr() % 16 == 0 and un.data_ptr() % 16 == 4
+            o1 = torch.full((batch, rows), float("nan"), dtype=torch.float32, device="cuda")
+            o2 = torch.full_like(o1, float("nan"))
+            h.matvec(xs, batch, o1, dtype=dt)
+            h.matvec(un, batch, o2, dtype=dt)
+            h.sync()
+            a, b = o1.cpu().numpy(), o2.cpu().numpy()
+            assert np.isfinite(a).all()
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (batch, bf16)
+    finally:
+        h.close()
+
+
+def test_folded_logits_big_head_matches_prepared():
+    """turbo_lmhead_logits on a head with many tiles folds the digit planes into the 16-tile
+    workgroup kernel; the same rows at an unaligned address take the preparation kernel."""
+    V, D = 262144, 2816
+    W, S, B, g = synth.make_head(V, D, 91)
+    h = T.LMHead(W, S, B, g, vocab=V, hidden=D, softcap=30.0)
+    try:
+        for batch in (1, 2):
+            x = torch.from_numpy(synth.hidden_states(batch, D, 92 + batch)).cuda()
+            flat = x.reshape(-1)
+            buf = torch.zeros(flat.numel() + 4, dtype=torch.float32, device="cuda")
+            buf[1:1 + flat.numel()] = flat
+            un = buf[1:1 + flat.numel()]
+            l1 = torch.full((batch, V), float("nan"), dtype=torch.float32, device="cuda")
+            l2 = torch.full_like(l1, float("nan"))
+            h.logits(x, batch, l1)
+            h.logits(un, batch, l2)
+            h.sync()
+            a, b = l1.cpu().numpy(), l2.cpu().numpy()
+            assert np.isfinite(a).all()
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), batch
+    finally:
+        h.close()

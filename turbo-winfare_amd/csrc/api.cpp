@@ -349,7 +349,7 @@ int run_rows(HandleBox& bx, const TurboStepInputs* in, const TurboStepOutputs* o
     // history is long enough that every workgroup scanning it would cost more than one kernel,
     // or the hidden rows are not 16-byte aligned (the fold reads them in 16-byte pieces).
     const bool fold = hidden && B <= tdt::kFusedRows && !has_bias && h.D <= tdt::kFusedMaxD &&
-                      h.ntile >= 2048u && (reinterpret_cast<uintptr_t>(hidden) & 15u) == 0u &&
+                      h.ntile >= tdt::kFusedMinTiles && (reinterpret_cast<uintptr_t>(hidden) & 15u) == 0u &&
                       (!has_hist || in->history_stride <= tdt::kFusedHistMax);
     if (fold) {
         tdt::FusedPrep fp{};
@@ -712,8 +712,26 @@ TURBO_DT_API int turbo_lmhead_logits(void* handle, const void* x, int x_dtype, i
         throw std::runtime_error("x_dtype must be TURBO_HIDDEN_F32 or TURBO_HIDDEN_BF16");
     tdt::DevRow rows[kMaxBatch];
     for (int b = 0; b < batch; ++b) rows[b] = greedy_devrow(h);
+    const tdt::EpiArgs ep = epi_args(h, logits, apply_softcap != 0);
+    // One or two 16-byte-aligned rows: the head kernel computes the digit planes itself (no
+    // preparation kernel), with one workgroup per 16 tiles or, for few tiles, per tile.
+    const uint32_t nt = tdt::split_threads(h);
+    const bool fold = batch <= tdt::kFusedRows && h.D <= tdt::kFusedMaxD &&
+                      (reinterpret_cast<uintptr_t>(x) & 15u) == 0u &&
+                      (h.ntile >= tdt::kFusedMinTiles || (nt && h.D <= 8u * nt));
+    if (fold) {
+        tdt::FusedPrep fp{};
+        fp.hidden = x;
+        fp.dtype = x_dtype == TURBO_HIDDEN_BF16 ? 1 : 0;
+        fp.normed = 1;
+        fp.eps = h.eps;
+        fp.rows_dst = h.rows;
+        for (int b = 0; b < batch; ++b) fp.inl[b] = rows[b];
+        launch_head(*bx, batch, ep, &fp);
+        return 1;
+    }
     simple_prep(h, rows, batch, x, x_dtype == TURBO_HIDDEN_BF16 ? 1 : 0, true, nullptr, path_for(batch));
-    launch_head(*bx, batch, epi_args(h, logits, apply_softcap != 0));
+    launch_head(*bx, batch, ep);
     return 1;
     API_CATCH(0)
 }

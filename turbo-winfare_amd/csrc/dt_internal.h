@@ -155,6 +155,9 @@ uint32_t modtable_sort_size(const Head& h, uint32_t n);
 constexpr int kFusedRows = 2;
 constexpr uint32_t kFusedMaxD = 8192;       // digit planes of a row in LDS: D / 32 * 24 words
 constexpr uint32_t kFusedHistMax = 4096;    // history stride scanned by every workgroup
+// Heads with fewer tiles fold the digit planes into the split kernel instead (normalised rows
+// without history only: the int4 matvec and logits entry points).
+constexpr uint32_t kFusedMinTiles = 2048;
 struct FusedPrep {
     const void* hidden;
     int dtype;                   // 0 fp32, 1 bf16
@@ -169,6 +172,8 @@ struct FusedPrep {
 };
 void launch_head_digits_fused(const Head& h, int batch, const FusedPrep& fp, const EpiArgs& ep,
                               hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
+// Threads per workgroup of the split digit kernel for this head (0: one wave per tile instead).
+uint32_t split_threads(const Head& h);
 
 // gemv_digits.hip / gemm_mfma.hip
 // ev0 / ev1 (may be null): timing events stamped by the head kernel's own dispatch

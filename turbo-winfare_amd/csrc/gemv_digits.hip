@@ -19,6 +19,7 @@
 
 #include <algorithm>
 #include <stdexcept>
+#include <type_traits>
 
 #include "dt_epilogue.h"
 
@@ -203,7 +204,7 @@ __device__ inline T octet_group_reduce(T v, Op op) {
 }
 
 template <int NB>
-__device__ void fused_prep(const FusedPrep& fp, uint32_t D, uint32_t V, const FusedIn<NB>& in, FusedLds<NB>& s) {
+__device__ __attribute__((always_inline)) inline void fused_prep(const FusedPrep& fp, uint32_t D, uint32_t V, const FusedIn<NB>& in, FusedLds<NB>& s) {
 #pragma clang fp contract(off)
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t idbase = blockIdx.x * kFusedThreads;
@@ -390,9 +391,20 @@ __global__ __launch_bounds__(kFusedThreads) void k_head_digits_fused(
     }
 }
 
+void launch_split_folded(const Head& h, int batch, const FusedPrep& fp, const EpiArgs& ep, hipStream_t st,
+                         hipEvent_t ev0, hipEvent_t ev1);
+
 void launch_head_digits_fused(const Head& h, int batch, const FusedPrep& fp, const EpiArgs& ep,
                               hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     if (h.D > kFusedMaxD || h.D % kGroup != 0u) throw std::runtime_error("folded step needs D <= 8192");
+    if (h.ntile < kFusedMinTiles) {
+        // few tiles: the split kernel with the digit planes folded in (normalised rows, no history)
+        const uint32_t nt = split_threads(h);
+        if (!nt || h.D > 8u * nt || !fp.normed || fp.history)
+            throw std::runtime_error("folded split head needs normalised rows, no history and D <= 8 x threads");
+        launch_split_folded(h, batch, fp, ep, st, ev0, ev1);
+        return;
+    }
     const dim3 grid((h.ntile + kFusedWaves - 1u) / kFusedWaves), block(kFusedThreads);
     if (batch == 1)
         hipExtLaunchKernelGGL(k_head_digits_fused<1>, grid, block, 0, st, ev0, ev1, 0, h.Wt, h.SBt, h.D, h.NC,
@@ -409,12 +421,18 @@ void launch_head_digits_fused(const Head& h, int batch, const FusedPrep& fp, con
 // parallelism: here a workgroup of KS waves shares one tile, wave w taking groups
 // [w G / KS, (w + 1) G / KS), and the partial sums are added in wave order through LDS before
 // wave 0 runs the epilogue.
+// FUSED: the digit planes of the (already normalised) rows are computed by every workgroup into
+// LDS from fp.hidden while its first weight groups are in flight, as in k_head_digits_fused,
+// instead of being read from a preparation kernel's output; the row parameters come from fp.inl.
+// Needs one thread per 8 elements of the row (D <= 8 KS 64).
 constexpr uint32_t kMaxSplit = 16;
-template <int NB>
+template <int NB, bool FUSED>
 __global__ __launch_bounds__(kMaxSplit * 64) void k_head_digits_split(
     const uint4* __restrict__ Wt, const uint32_t* __restrict__ SBt, const uint32_t* __restrict__ xdig,
-    const float* __restrict__ xws, const float* __restrict__ xsum, uint32_t NC, uint32_t G, EpiArgs ep) {
+    const float* __restrict__ xws, const float* __restrict__ xsum, uint32_t NC, uint32_t G, EpiArgs ep,
+    FusedPrep fp, uint32_t D) {
     __shared__ float part[kMaxSplit][NB][64];
+    __shared__ __attribute__((aligned(16))) std::conditional_t<FUSED, FusedLds<NB>, uint32_t> fs;
     // wave-uniform by construction; read through the scalar unit so the group range, and with it
     // the digit-word addresses, stay scalar (s_load) instead of per-lane loads
     const uint32_t lane = threadIdx.x & 63u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -429,9 +447,9 @@ __global__ __launch_bounds__(kMaxSplit * 64) void k_head_digits_split(
     // a wave holds few groups: all of a batch of kBatchG are loaded before any is used, so
     // the wave waits for memory once per batch rather than once per group
     constexpr uint32_t kBatchG = 4;
-    for (uint32_t gb = g0; gb < g1; gb += kBatchG) {
-        uint4 Ab[kBatchG], Bb[kBatchG];
-        uint32_t Sb[kBatchG];
+    uint4 Ab[kBatchG], Bb[kBatchG];
+    uint32_t Sb[kBatchG];
+    auto load_batch = [&](uint32_t gb) {
 #pragma unroll
         for (uint32_t q = 0; q < kBatchG; ++q) {
             const uint32_t g = min(gb + q, g1 - 1u);  // past the range: a repeated, unused load
@@ -439,6 +457,20 @@ __global__ __launch_bounds__(kMaxSplit * 64) void k_head_digits_split(
             Bb[q] = load_stream(wp + (size_t)(2 * g + 1) * kTileRows);
             Sb[q] = load_stream(sbp + (size_t)g * kTileRows);
         }
+    };
+    // every wave holds at least one group (KS <= G)
+    [[maybe_unused]] FusedIn<NB> in;
+    if constexpr (FUSED) {
+        fused_load<NB>(fp, D, in);
+        __builtin_amdgcn_sched_barrier(0);  // the row's loads ahead of the weight batch
+    }
+    load_batch(g0);
+    if constexpr (FUSED) {
+        __builtin_amdgcn_sched_barrier(0);
+        fused_prep<NB>(fp, D, ep.V, in, fs);
+    }
+    for (uint32_t gb = g0; gb < g1; gb += kBatchG) {
+        if (gb != g0) load_batch(gb);
 #pragma unroll
         for (uint32_t q = 0; q < kBatchG; ++q) {
             // branch-free: a group past the range is computed on its clamped copy and dropped,
@@ -455,7 +487,17 @@ __global__ __launch_bounds__(kMaxSplit * 64) void k_head_digits_split(
             const float c8 = fmaf(8.0f, sf, bf);
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
-                const uint32_t* xd = xdig + ((size_t)nb * NC + 2u * g) * kDigitWordsPerChunk;
+                const uint32_t* xd;
+                float ws, sm;
+                if constexpr (FUSED) {
+                    xd = &fs.dig[nb][(2u * g) * kDigitWordsPerChunk];
+                    ws = fs.ws[nb][g];
+                    sm = fs.sum[nb][g];
+                } else {
+                    xd = xdig + ((size_t)nb * NC + 2u * g) * kDigitWordsPerChunk;
+                    ws = xws[(size_t)nb * G + g];
+                    sm = xsum[(size_t)nb * G + g];
+                }
                 int a[kDigits];
 #pragma unroll
                 for (uint32_t k = 0; k < kDigits; ++k) a[k] = 0;
@@ -470,8 +512,8 @@ __global__ __launch_bounds__(kMaxSplit * 64) void k_head_digits_split(
                 uint32_t Dg = (uint32_t)a[0];
 #pragma unroll
                 for (uint32_t k = 1; k < kDigits; ++k) Dg += (uint32_t)a[k] << (4u * k);
-                float t = fmaf((float)(int)Dg, sf * xws[(size_t)nb * G + g], acc[nb]);
-                t = fmaf(c8, xsum[(size_t)nb * G + g], t);
+                float t = fmaf((float)(int)Dg, sf * ws, acc[nb]);
+                t = fmaf(c8, sm, t);
                 acc[nb] = in ? t : acc[nb];
             }
         }
@@ -484,22 +526,46 @@ __global__ __launch_bounds__(kMaxSplit * 64) void k_head_digits_split(
     for (int nb = 0; nb < NB; ++nb) {
         float v = part[0][nb][lane];
         for (uint32_t w = 1; w < KS; ++w) v += part[w][nb][lane];
-        epilogue_wave(v, (uint32_t)nb, tile, lane, ep);
+        if constexpr (FUSED) epilogue_wave_counted(v, (uint32_t)nb, tile, lane, ep, fp.inl[nb], 0u);
+        else epilogue_wave(v, (uint32_t)nb, tile, lane, ep);
     }
+}
+
+// Workgroup size of the split kernel for this head: 64 * KS threads, or 0 when the head takes
+// one wave per tile instead. Enough waves to fill the chip (~2048) from few tiles.
+uint32_t split_threads(const Head& h) {
+    const uint32_t ks = std::min<uint32_t>({kMaxSplit, h.G, (2048u + h.ntile - 1u) / h.ntile});
+    return ks >= 2u ? 64u * ks : 0u;
+}
+
+void launch_split_folded(const Head& h, int batch, const FusedPrep& fp, const EpiArgs& ep, hipStream_t st,
+                         hipEvent_t ev0, hipEvent_t ev1) {
+    const dim3 grid(h.ntile), block(split_threads(h));
+    const uint32_t* no_dig = nullptr;
+    const float* no_f = nullptr;
+    if (batch == 1)
+        hipExtLaunchKernelGGL((k_head_digits_split<1, true>), grid, block, 0, st, ev0, ev1, 0, h.Wt, h.SBt, no_dig,
+                              no_f, no_f, h.NC, h.G, ep, fp, h.D);
+    else if (batch == 2)
+        hipExtLaunchKernelGGL((k_head_digits_split<2, true>), grid, block, 0, st, ev0, ev1, 0, h.Wt, h.SBt, no_dig,
+                              no_f, no_f, h.NC, h.G, ep, fp, h.D);
+    else
+        throw std::runtime_error("folded step supports batch 1 or 2");
+    check_hip(hipGetLastError(), "head (digit GEMV, split groups, folded digits)");
 }
 
 void launch_head_digits(const Head& h, int batch, const EpiArgs& ep, hipStream_t st,
                         hipEvent_t ev0, hipEvent_t ev1) {
-    // enough waves to fill the chip (~2048) from few tiles: split each tile's groups
-    const uint32_t ks = std::min<uint32_t>({kMaxSplit, h.G, (2048u + h.ntile - 1u) / h.ntile});
-    if (ks >= 2u && (batch == 1 || batch == 2)) {
-        const dim3 grid(h.ntile), block(64u * ks);
+    const uint32_t nt = split_threads(h);
+    if (nt && (batch == 1 || batch == 2)) {
+        const dim3 grid(h.ntile), block(nt);
+        const FusedPrep none{};
         if (batch == 1)
-            hipExtLaunchKernelGGL(k_head_digits_split<1>, grid, block, 0, st, ev0, ev1, 0, h.Wt, h.SBt, h.xdig,
-                                  h.xws, h.xsum, h.NC, h.G, ep);
+            hipExtLaunchKernelGGL((k_head_digits_split<1, false>), grid, block, 0, st, ev0, ev1, 0, h.Wt, h.SBt,
+                                  h.xdig, h.xws, h.xsum, h.NC, h.G, ep, none, h.D);
         else
-            hipExtLaunchKernelGGL(k_head_digits_split<2>, grid, block, 0, st, ev0, ev1, 0, h.Wt, h.SBt, h.xdig,
-                                  h.xws, h.xsum, h.NC, h.G, ep);
+            hipExtLaunchKernelGGL((k_head_digits_split<2, false>), grid, block, 0, st, ev0, ev1, 0, h.Wt, h.SBt,
+                                  h.xdig, h.xws, h.xsum, h.NC, h.G, ep, none, h.D);
         check_hip(hipGetLastError(), "head (digit GEMV, split groups)");
         return;
     }
