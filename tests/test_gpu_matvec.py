@@ -74,6 +74,14 @@ def test_folded_matvec_matches_prepared(rows, in_dim, bf16):
             a, b = o1.cpu().numpy(), o2.cpu().numpy()
             assert np.isfinite(a).all()
             assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (batch, bf16)
+            # the greedy entry folds the same way; its select reads the rows the head stored
+            t1 = torch.full((batch,), -1, dtype=torch.int32, device="cuda")
+            t2 = torch.full_like(t1, -1)
+            h.greedy(xs, batch, t1, dtype=dt)
+            h.greedy(un, batch, t2, dtype=dt)
+            h.sync()
+            want = [int(np.argmax(a[r])) for r in range(batch)]  # no softcap on this head
+            assert t1.cpu().tolist() == want and t2.cpu().tolist() == want, (batch, bf16)
     finally:
         h.close()
 
@@ -99,5 +107,12 @@ def test_folded_logits_big_head_matches_prepared():
             a, b = l1.cpu().numpy(), l2.cpu().numpy()
             assert np.isfinite(a).all()
             assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), batch
+            t1 = torch.full((batch,), -1, dtype=torch.int32, device="cuda")
+            t2 = torch.full_like(t1, -1)
+            h.greedy(x, batch, t1)
+            h.greedy(un, batch, t2)
+            h.sync()
+            want = [int(np.argmax(a[r])) for r in range(batch)]  # argmax of the softcapped logits
+            assert t1.cpu().tolist() == want and t2.cpu().tolist() == want, batch
     finally:
         h.close()

@@ -302,6 +302,32 @@ void launch_head(HandleBox& bx, int B, const tdt::EpiArgs& ep, const tdt::FusedP
 
 tdt::HeadPath path_for(int B) { return B <= 2 ? tdt::HeadPath::Digits : tdt::HeadPath::Mfma; }
 
+// The head over normalised rows x with greedy row parameters (turbo_lmhead_logits,
+// turbo_int4_matvec, turbo_lmhead_greedy). One or two 16-byte-aligned rows: the head kernel
+// computes the digit planes itself (no preparation kernel), with one workgroup per 16 tiles or,
+// for few tiles, per tile; it also stores the rows for a select kernel that follows.
+void launch_greedy_head(HandleBox& bx, const tdt::DevRow* rows, int batch, const void* x, int x_dtype,
+                        const tdt::EpiArgs& ep) {
+    Head& h = bx.h;
+    const uint32_t nt = tdt::split_threads(h);
+    const bool fold = batch <= tdt::kFusedRows && h.D <= tdt::kFusedMaxD &&
+                      (reinterpret_cast<uintptr_t>(x) & 15u) == 0u &&
+                      (h.ntile >= tdt::kFusedMinTiles || (nt && h.D <= 8u * nt));
+    if (fold) {
+        tdt::FusedPrep fp{};
+        fp.hidden = x;
+        fp.dtype = x_dtype == TURBO_HIDDEN_BF16 ? 1 : 0;
+        fp.normed = 1;
+        fp.eps = h.eps;
+        fp.rows_dst = h.rows;
+        for (int b = 0; b < batch; ++b) fp.inl[b] = rows[b];
+        launch_head(bx, batch, ep, &fp);
+        return;
+    }
+    simple_prep(h, rows, batch, x, x_dtype == TURBO_HIDDEN_BF16 ? 1 : 0, true, nullptr, path_for(batch));
+    launch_head(bx, batch, ep);
+}
+
 void check_batch(const Head& h, int B) {
     if (B < 1 || B > h.max_batch)
         throw std::runtime_error("batch must be in 1.." + std::to_string(h.max_batch));
@@ -712,26 +738,7 @@ TURBO_DT_API int turbo_lmhead_logits(void* handle, const void* x, int x_dtype, i
         throw std::runtime_error("x_dtype must be TURBO_HIDDEN_F32 or TURBO_HIDDEN_BF16");
     tdt::DevRow rows[kMaxBatch];
     for (int b = 0; b < batch; ++b) rows[b] = greedy_devrow(h);
-    const tdt::EpiArgs ep = epi_args(h, logits, apply_softcap != 0);
-    // One or two 16-byte-aligned rows: the head kernel computes the digit planes itself (no
-    // preparation kernel), with one workgroup per 16 tiles or, for few tiles, per tile.
-    const uint32_t nt = tdt::split_threads(h);
-    const bool fold = batch <= tdt::kFusedRows && h.D <= tdt::kFusedMaxD &&
-                      (reinterpret_cast<uintptr_t>(x) & 15u) == 0u &&
-                      (h.ntile >= tdt::kFusedMinTiles || (nt && h.D <= 8u * nt));
-    if (fold) {
-        tdt::FusedPrep fp{};
-        fp.hidden = x;
-        fp.dtype = x_dtype == TURBO_HIDDEN_BF16 ? 1 : 0;
-        fp.normed = 1;
-        fp.eps = h.eps;
-        fp.rows_dst = h.rows;
-        for (int b = 0; b < batch; ++b) fp.inl[b] = rows[b];
-        launch_head(*bx, batch, ep, &fp);
-        return 1;
-    }
-    simple_prep(h, rows, batch, x, x_dtype == TURBO_HIDDEN_BF16 ? 1 : 0, true, nullptr, path_for(batch));
-    launch_head(*bx, batch, ep);
+    launch_greedy_head(*bx, rows, batch, x, x_dtype, epi_args(h, logits, apply_softcap != 0));
     return 1;
     API_CATCH(0)
 }
@@ -749,8 +756,7 @@ TURBO_DT_API int turbo_lmhead_greedy(void* handle, const void* x, int x_dtype, i
         throw std::runtime_error("x_dtype must be TURBO_HIDDEN_F32 or TURBO_HIDDEN_BF16");
     tdt::DevRow rows[kMaxBatch];
     for (int b = 0; b < batch; ++b) rows[b] = greedy_devrow(h);
-    simple_prep(h, rows, batch, x, x_dtype == TURBO_HIDDEN_BF16 ? 1 : 0, true, nullptr, path_for(batch));
-    launch_head(*bx, batch, epi_args(h, nullptr, true));
+    launch_greedy_head(*bx, rows, batch, x, x_dtype, epi_args(h, nullptr, true));
     tdt::SelectArgs sa{};
     sa.V = h.V;
     sa.ntile = h.ntile;

@@ -529,6 +529,11 @@ __global__ __launch_bounds__(kMaxSplit * 64) void k_head_digits_split(
         if constexpr (FUSED) epilogue_wave_counted(v, (uint32_t)nb, tile, lane, ep, fp.inl[nb], 0u);
         else epilogue_wave(v, (uint32_t)nb, tile, lane, ep);
     }
+    // the row parameters for a select kernel that may follow (workgroup 0, after its stream)
+    if constexpr (FUSED) {
+        if (blockIdx.x == 0u && fp.rows_dst && lane < NB * (sizeof(DevRow) / 4))
+            reinterpret_cast<uint32_t*>(fp.rows_dst)[lane] = reinterpret_cast<const uint32_t*>(&fp.inl[0])[lane];
+    }
 }
 
 // Workgroup size of the split kernel for this head: 64 * KS threads, or 0 when the head takes
