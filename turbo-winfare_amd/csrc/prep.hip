@@ -81,15 +81,19 @@ void launch_repack(const Head& h, const uint8_t* W, const uint16_t* S, const uin
 // (x0, x4, x1/16, x5/16, x2, x6, x3/16, x7/16): the order in which the weight dequant produces
 // halves, with odd elements divided by 16 because their weight halves carry a factor 16.
 //
-// History counts: every history occurrence with id < V adds one to hcount[b][id] and sets the
-// id's bit in hbits[b] (global atomics); the head epilogue zeroes both as it reads them, so
-// they are zero between steps.
+// History counts: the occurrences of each id < V (merged per id in LDS first) are added to
+// hcount[b][id] and the id's bit is set in hbits[b] (global atomics); the head epilogue zeroes
+// both as it reads them, so they are zero between steps.
 // Bias table: the bias entries are sorted by (id, list position) with a bitonic sort in LDS;
 // each run of equal ids becomes one entry whose value is the run's biases summed in list order
 // from 0.0f. Entries are written sorted by id; block_start[t] = number of entries with
 // id < 64 t comes from a binary search over the run ids.
 constexpr uint32_t kPrepThreads = 1024;
 constexpr uint32_t kPrepWaves = kPrepThreads / 64;
+// LDS table merging a row's history occurrences per id: 2^kHistSlotBits slots of (id, count).
+constexpr uint32_t kHistSlotBits = 11;
+constexpr uint32_t kHistSlots = 1u << kHistSlotBits;
+static_assert(kHistSlots <= kPrepPoolU64, "the history table lives in the prep kernel's LDS pool");
 
 // RMSNorm block k of row b: every block sums the squares of the whole row (the row is small and
 // L2-resident; all blocks of a row compute the same sum in the same order), then normalises and
@@ -179,16 +183,41 @@ __device__ void modtable_row(const PrepArgs& a, uint32_t b, unsigned long long* 
     const uint32_t V = a.V;
     if ((use & 1u) && a.history) {
         // One count per occurrence (src/sampling.cpp:81-89 visits every occurrence); ids past
-        // the vocabulary are ignored (:82).
+        // the vocabulary are ignored (:82). Occurrences are first merged per id in an LDS table
+        // (one slot per hash of the id; an occurrence whose slot holds another id goes straight
+        // to the global counters), so a frequent id costs one global atomic instead of one per
+        // occurrence: same-address global atomics serialise in L2.
+        uint32_t* hk = reinterpret_cast<uint32_t*>(keys);  // [kHistSlots] ids, ~0 when empty
+        uint32_t* hc = hk + kHistSlots;                     // [kHistSlots] occurrence counts
+        for (uint32_t i = tid; i < kHistSlots; i += kPrepThreads) {
+            hk[i] = ~0u;
+            hc[i] = 0u;
+        }
+        __syncthreads();
         const uint32_t nh = min(a.hist_len[b], a.hist_stride);
         const uint32_t* hist = a.history + (size_t)b * a.hist_stride;
         for (uint32_t i = tid; i < nh; i += kPrepThreads) {
             const uint32_t id = hist[i];
             if (id < V) {
-                atomicAdd(a.hcount + (size_t)b * V + id, 1u);
+                const uint32_t slot = (id * 2654435761u) >> (32u - kHistSlotBits);
+                const uint32_t prev = atomicCAS(&hk[slot], ~0u, id);
+                if (prev == ~0u || prev == id) {
+                    atomicAdd(&hc[slot], 1u);
+                } else {
+                    atomicAdd(a.hcount + (size_t)b * V + id, 1u);
+                    atomicOr(a.hbits + (size_t)b * a.hbw + (id >> 5), 1u << (id & 31u));
+                }
+            }
+        }
+        __syncthreads();
+        for (uint32_t i = tid; i < kHistSlots; i += kPrepThreads) {
+            const uint32_t id = hk[i];
+            if (id != ~0u) {
+                atomicAdd(a.hcount + (size_t)b * V + id, hc[i]);
                 atomicOr(a.hbits + (size_t)b * a.hbw + (id >> 5), 1u << (id & 31u));
             }
         }
+        __syncthreads();  // the bias table below reuses the pool
     }
     if (!(use & 2u) || !a.bias_ids) return;
     const uint32_t P = a.P;
