@@ -364,7 +364,7 @@ __device__ inline uint32_t select_tied_id(SelShared& s, const uint2* list, uint3
 
 // First element of set `ps`, in (key desc, id asc) order, whose cumulative weight reaches
 // `target`. Returns 1 with (*kx, *ix); 0 when the set's total weight is below target.
-__device__ int find_cross(SelShared& s, const RowCtx& c, const PSet& ps, int mode, double target,
+__device__ __attribute__((always_inline)) inline int find_cross(SelShared& s, const RowCtx& c, const PSet& ps, int mode, double target,
                           uint32_t* kx, uint32_t* ix) {
     const uint32_t tid = threadIdx.x;
     for (uint32_t i = tid; i < kBins; i += sel_nt()) s.hd[i] = 0ull;
@@ -556,7 +556,7 @@ __device__ __attribute__((always_inline)) inline void fv_gather(SelShared& s, co
 // level of 2048 sub-bins over the bin's value range (u64 fixed-point weights) locates the
 // crossing; only that sub-bin's elements are then sorted and summed exactly. Returns 1 with the
 // element's key and the weight before it; 0 when the sub-bin holds more than 1024 elements.
-__device__ int fine_cross(SelShared& s, const RowCtx& c, uint32_t n, uint32_t bin, unsigned long long key_limit,
+__device__ __attribute__((always_inline)) inline int fine_cross(SelShared& s, const RowCtx& c, uint32_t n, uint32_t bin, unsigned long long key_limit,
                           float kw, double target, unsigned long long* key_out, double* before_out) {
     const uint32_t tid = threadIdx.x;
     unsigned long long* hf = reinterpret_cast<unsigned long long*>(s.pkey);   // 2048 sub-bins
@@ -633,7 +633,7 @@ __device__ int fine_cross(SelShared& s, const RowCtx& c, uint32_t n, uint32_t bi
 }
 
 // Sum of exp2((v - m) * kw) over the candidates of `bin` with key <= key_limit.
-__device__ double bin_weight(SelShared& s, const RowCtx& c, uint32_t n, uint32_t bin, unsigned long long key_limit, float kw) {
+__device__ __attribute__((always_inline)) inline double bin_weight(SelShared& s, const RowCtx& c, uint32_t n, uint32_t bin, unsigned long long key_limit, float kw) {
     double acc = 0.0;
     for (uint32_t e = threadIdx.x; e < n; e += sel_nt()) {
         const unsigned long long k = s.cand[e];
@@ -647,7 +647,7 @@ __device__ double bin_weight(SelShared& s, const RowCtx& c, uint32_t n, uint32_t
 // From the n gathered candidates in s.cand (unsorted) and the histograms in s.vm / s.vq: the
 // nucleus cut inside bin cb and the temperature draw. Returns 1 with *token, 0 when rounding
 // put the draw outside the gathered bins or a sub-bin is a massive tie (radix fallback).
-__device__ int fv_finish(SelShared& s, const RowCtx& c, const FvPlan& P, uint32_t n, float u,
+__device__ __attribute__((always_inline)) inline int fv_finish(SelShared& s, const RowCtx& c, const FvPlan& P, uint32_t n, float u,
                          uint32_t* token, double* denom_out, double* r_out) {
     const float kq = kLog2e / c.T;
     const unsigned long long* hq = same_weights(c) ? s.vm : s.vq;
@@ -701,7 +701,7 @@ __device__ __attribute__((always_inline)) inline int full_vocab_value_path(SelSh
 }
 
 // Radix fallback over the whole row: shortlist bound, nucleus, then the draw.
-__device__ void radix_select(SelShared& s, const RowCtx& c, const DevRow& row, float u, uint32_t want,
+__device__ __attribute__((always_inline)) inline void radix_select(SelShared& s, const RowCtx& c, const DevRow& row, float u, uint32_t want,
                              double Z, uint32_t arg, uint32_t* token, RowReport* rep) {
     uint32_t kx, ix;
     PSet s0 = {0, 0u, 0u};
