@@ -113,6 +113,8 @@ TURBO_DT_API void* turbo_lmhead_create(const TurboLMHeadDesc* desc);
 TURBO_DT_API void turbo_lmhead_destroy(void* handle);
 /* hip_stream is a hipStream_t (NULL = the null stream). Must be created at default priority. */
 TURBO_DT_API int turbo_lmhead_set_stream(void* handle, void* hip_stream);
+/* Waits for the handle's stream. Returns 0 (once) when a step since the last call found a full
+ * history under TURBO_STEP_APPEND_HISTORY (TURBO_STATUS_HISTORY_FULL). */
 TURBO_DT_API int turbo_lmhead_synchronize(void* handle);
 /* Largest batch one step accepts, and the largest bias_stride (logit-bias entries per row).
  * History length is not limited. */
@@ -168,7 +170,14 @@ enum { TURBO_HIDDEN_F32 = 0, TURBO_HIDDEN_BF16 = 1 };
 enum {
     TURBO_STEP_NORMED = 1u,          /* hidden is already normalised: skip the final RMSNorm */
     TURBO_STEP_APPEND_HISTORY = 2u   /* append each row's token to its history on the device
-                                        (src/runner.cpp:878), incrementing history_len */
+                                        (src/runner.cpp:878), incrementing history_len. The
+                                        reference's history grows without bound; here it holds
+                                        history_stride ids per row, so the caller sizes the
+                                        stride for the initial length plus every step it will
+                                        run. A row whose history is full keeps its token but
+                                        does not append it: its report has
+                                        TURBO_STATUS_HISTORY_FULL and the next
+                                        turbo_lmhead_synchronize returns 0 with the reason. */
 };
 
 /* Row-strided side inputs. Any group may be NULL / zero to disable it. */
@@ -207,7 +216,15 @@ typedef struct {
     double total;           /* sum exp(l - max) over the row */
     double denom;           /* survivor weight sum */
     double r;               /* u * denom */
+    uint32_t status;        /* TURBO_STATUS_* bits */
+    uint32_t reserved;
 } TurboRowReport;
+
+enum {
+    /* TURBO_STEP_APPEND_HISTORY found history_len == history_stride: the token was returned but
+     * not appended. turbo_lmhead_synchronize then fails (once) with the row in the message. */
+    TURBO_STATUS_HISTORY_FULL = 1u
+};
 
 typedef struct {
     uint32_t* tokens;        /* [batch]; 0xFFFFFFFF marks a degenerate distribution */

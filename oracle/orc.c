@@ -12,6 +12,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 
 /* ---- numeric primitives ---------------------------------------------------------------- */
 
@@ -472,4 +473,40 @@ void orc_apply_modifiers(float* logits, uint32_t vocab, const orc_params* p, flo
                                      p->frequency_penalty);
     }
     if (ban_words) orc_apply_ban(logits, vocab, ban_words);
+}
+
+/* ---- timed decode loop (CPU baseline of the benchmark) ---------------------------------- */
+
+static double now_seconds(void) {
+    struct timespec t;
+    clock_gettime(CLOCK_MONOTONIC, &t);
+    return (double)t.tv_sec + 1e-9 * (double)t.tv_nsec;
+}
+
+int orc_time_decode_steps(const uint8_t* W, const uint16_t* S, const uint16_t* B, const uint16_t* gamma,
+                          uint32_t vocab, uint32_t in_dim, float eps, float softcap, const float* hidden,
+                          uint32_t nsteps, uint64_t first_counter, int threads, const orc_params* p,
+                          uint64_t seed, uint32_t* history, size_t history_len, size_t history_cap,
+                          uint32_t* tokens, double* seconds) {
+    float* xn = (float*)malloc(sizeof(float) * in_dim);
+    float* l = (float*)malloc(sizeof(float) * vocab);
+    if (!xn || !l) {
+        free(xn);
+        free(l);
+        return 0;
+    }
+    for (uint32_t s = 0; s < nsteps; ++s) {
+        const double t0 = now_seconds();
+        orc_rms_norm(hidden + (size_t)s * in_dim, gamma, in_dim, eps, xn);
+        orc_matvec_int4_mt(W, S, B, vocab, in_dim, xn, l, threads);
+        orc_softcap(l, vocab, softcap);
+        orc_apply_modifiers(l, vocab, p, softcap, history, history_len, NULL, NULL, 0, NULL);
+        const uint32_t tok = orc_sample_token_u(l, vocab, p, orc_philox_uniform(seed, first_counter + s), NULL);
+        if (history_len < history_cap) history[history_len++] = tok;
+        seconds[s] = now_seconds() - t0;
+        tokens[s] = tok;
+    }
+    free(xn);
+    free(l);
+    return 1;
 }

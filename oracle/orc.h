@@ -165,6 +165,22 @@ void orc_apply_modifiers(float* logits, uint32_t vocab, const orc_params* p, flo
                          const uint32_t* bias_ids, const float* bias_values, size_t bias_count,
                          const uint32_t* ban_words);
 
+
+/* ---- timed decode loop (the benchmark's CPU baseline; not a restatement) ----------------- */
+
+/* Runs nsteps decode-tail steps of one row exactly as the reference CPU path chains them
+ * (src/cpu_reference.cpp:527-539 then :578-586): orc_rms_norm -> orc_matvec_int4_mt (`threads`
+ * POSIX threads, row-parallel) -> orc_softcap -> orc_apply_modifiers (history only) ->
+ * orc_sample_token_u with the Philox uniform (seed, first_counter + s), appending each token to
+ * history while history_len < history_cap. hidden is [nsteps][in_dim]. seconds[s] is the
+ * CLOCK_MONOTONIC duration of step s (hidden state in, token out). Returns 1, or 0 when a
+ * buffer cannot be allocated. */
+int orc_time_decode_steps(const uint8_t* W, const uint16_t* S, const uint16_t* B, const uint16_t* gamma,
+                          uint32_t vocab, uint32_t in_dim, float eps, float softcap, const float* hidden,
+                          uint32_t nsteps, uint64_t first_counter, int threads, const orc_params* p,
+                          uint64_t seed, uint32_t* history, size_t history_len, size_t history_cap,
+                          uint32_t* tokens, double* seconds);
+
 #ifdef __cplusplus
 }
 #endif

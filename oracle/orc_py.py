@@ -101,6 +101,11 @@ def orc() -> C.CDLL:
         lib.orc_apply_modifiers.argtypes = [_f32p, C.c_uint32, C.POINTER(Params), C.c_float,
                                             C.c_void_p, C.c_size_t, C.c_void_p, C.c_void_p,
                                             C.c_size_t, C.c_void_p]
+        lib.orc_time_decode_steps.restype = C.c_int
+        lib.orc_time_decode_steps.argtypes = [_u8p, _u16p, _u16p, C.c_void_p, C.c_uint32, C.c_uint32,
+                                              C.c_float, C.c_float, _f32p, C.c_uint32, C.c_uint64, C.c_int,
+                                              C.POINTER(Params), C.c_uint64, _u32p, C.c_size_t, C.c_size_t,
+                                              _u32p, np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")]
         _orc = lib
     return _orc
 
@@ -191,3 +196,25 @@ def philox_uniform(seed: int, counter: int) -> float:
 def reference_uniform(has_seed: int, seed: int, position: int) -> float:
     s = C.c_uint64(orc().orc_seed_for(has_seed, seed, position))
     return float(orc().orc_next_uniform(C.byref(s)))
+
+
+def time_decode_steps(W, S, B, gamma, hidden, p: Params, seed: int, history, *, first_counter=0,
+                      threads=1, eps=1e-6, cap=30.0):
+    """Runs hidden.shape[0] decode steps of one row in C (RMSNorm -> head -> softcap ->
+    modifiers -> sampler, the token appended to the history) and returns (tokens, seconds per
+    step). The timing is taken inside the C loop; no Python runs between its clock reads."""
+    hidden = np.ascontiguousarray(hidden, dtype=np.float32)
+    n, D = hidden.shape
+    V = W.shape[0]
+    hist = np.zeros(len(history) + n, dtype=np.uint32)
+    hist[:len(history)] = history
+    toks = np.zeros(n, dtype=np.uint32)
+    secs = np.zeros(n, dtype=np.float64)
+    g = None if gamma is None else np.ascontiguousarray(gamma, dtype=np.uint16)
+    ok = orc().orc_time_decode_steps(np.ascontiguousarray(W), np.ascontiguousarray(S), np.ascontiguousarray(B),
+                                     None if g is None else g.ctypes.data, V, D, eps, cap, hidden, n,
+                                     first_counter, threads, C.byref(p), seed, hist, len(history), hist.size,
+                                     toks, secs)
+    if not ok:
+        raise MemoryError("orc_time_decode_steps: allocation failed")
+    return toks, secs

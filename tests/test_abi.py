@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_struct_layouts():
     assert C.sizeof(T.TurboSamplingRow) == 56
-    assert C.sizeof(T.TurboRowReport) == 48
+    assert C.sizeof(T.TurboRowReport) == 56
     assert C.sizeof(T.TurboStepOutputs) == 24
 
 

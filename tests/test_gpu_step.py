@@ -44,7 +44,7 @@ def run_step(h, batch, rows, hidden, **kw):
     inp, keep = h.make_inputs(batch, rows, hidden=hidden, **kw)
     tok = torch.zeros(batch, dtype=torch.int32, device="cuda")
     logits = torch.empty((batch, V), dtype=torch.float32, device="cuda")
-    rep = torch.zeros((batch, 48 // 4), dtype=torch.int32, device="cuda")
+    rep = torch.zeros((batch, 56 // 4), dtype=torch.int32, device="cuda")
     h.step(inp, tok, logits, rep)
     h.sync()
     return tok.cpu().numpy().astype(np.uint32), logits.cpu().numpy()
@@ -222,7 +222,7 @@ def sample_given(h, logits_np, rows, **kw):
     lt = dev(logits_np)
     inp, keep = h.make_inputs(Bn, rows, **kw)
     tok = torch.zeros(Bn, dtype=torch.int32, device="cuda")
-    rep = torch.zeros((Bn, 12), dtype=torch.int32, device="cuda")
+    rep = torch.zeros((Bn, 56 // 4), dtype=torch.int32, device="cuda")
     h.sample_logits(lt, inp, tok, rep)
     h.sync()
     return tok.cpu().numpy().astype(np.uint32), lt.cpu().numpy(), rep.cpu().numpy()
@@ -549,3 +549,35 @@ def test_sampler_vocabulary_past_register_tiles(kind):
         assert paths[0] == 0 and all(paths[i] == 1 for i in (1, 2, 3)) and all(paths[i] == 2 for i in (4, 5))
     finally:
         h.close()
+
+
+def test_full_history_reports_and_fails_the_next_sync(head):
+    """TURBO_STEP_APPEND_HISTORY on a row whose history already holds history_stride ids: the
+    token is still produced, but not appended (history_len unchanged); the row's report carries
+    TURBO_STATUS_HISTORY_FULL and the next synchronisation fails once, naming the row. A row with
+    room appends as usual in the same step."""
+    h, _ = head
+    Bn = 2
+    x = dev(synth.hidden_states(Bn, D, SEED + 95))
+    stride = 64
+    hb = synth.uniform_ids(Bn * stride, V, SEED + 96).reshape(Bn, stride).astype(np.int32)
+    hist = dev(hb)
+    hl = torch.tensor([stride, 10], dtype=torch.int32, device="cuda")  # row 0 full, row 1 not
+    rows = [T.row_default(temperature=0.8, top_k=40, top_p=0.9, repetition_penalty=1.1, seed=3 + b, counter=1)
+            for b in range(Bn)]
+    inp, keep = h.make_inputs(Bn, rows, hidden=x, flags=T.TURBO_STEP_APPEND_HISTORY, history=hist,
+                              history_len=hl)
+    tok = torch.zeros(Bn, dtype=torch.int32, device="cuda")
+    rep = torch.zeros((Bn, 56 // 4), dtype=torch.int32, device="cuda")
+    h.step(inp, tok, None, rep)
+    with pytest.raises(T.TurboError, match="history full: row 0"):
+        h.sync()
+    h.sync()  # reported once
+    st = rep.cpu().numpy().view(np.uint32)[:, 12]  # TurboRowReport.status
+    assert st[0] == T.TURBO_STATUS_HISTORY_FULL and st[1] == 0, st
+    n = hl.cpu().numpy()
+    assert n[0] == stride and n[1] == 11, n
+    got = hist.cpu().numpy()
+    assert np.array_equal(got[0], hb[0])
+    assert got[1, 10] == int(tok[1].item())
+    assert int(tok[0].item()) < V

@@ -161,6 +161,7 @@ void free_head(Head& h) {
     dfree(h.fv_cand);
     dfree(h.fv_state);
     if (h.ring_host) (void)hipHostFree(h.ring_host);
+    if (h.overflow_host) (void)hipHostFree(h.overflow_host);
     for (int i = 0; i < Head::kRing / Head::kRingGroup; ++i)
         if (h.ring_ev[i]) (void)hipEventDestroy(h.ring_ev[i]);
     for (int i = 0; i < Head::kTimerSlots; ++i) {
@@ -333,11 +334,16 @@ void check_batch(const Head& h, int B) {
         throw std::runtime_error("batch must be in 1.." + std::to_string(h.max_batch));
 }
 
-// Shared by turbo_lmhead_step and turbo_sample_logits.
-int run_rows(HandleBox& bx, const TurboStepInputs* in, const TurboStepOutputs* out,
+}  // namespace
+
+namespace tdt {
+
+// Shared by turbo_lmhead_step, turbo_sample_logits and turbo_sample_logits_noalloc. bx (the
+// handle, for head-kernel timing) may be null when hidden is null: no head kernel runs then.
+int run_rows(Head& h, HandleBox* bx, const TurboStepInputs* in, const TurboStepOutputs* out,
              const void* hidden, float* given_logits) {
-    Head& h = bx.h;
     if (!in || !out) throw std::runtime_error("null inputs or outputs");
+    if (hidden && !bx) throw std::runtime_error("a head step needs a handle");
     const int B = in->batch;
     check_batch(h, B);
     if (!in->rows) throw std::runtime_error("rows is NULL");
@@ -395,7 +401,7 @@ int run_rows(HandleBox& bx, const TurboStepInputs* in, const TurboStepOutputs* o
         ep.no_sumexp = any_short ? 0u : 1u;
         ep.ban = in->ban_bits;
         ep.ban_stride = in->ban_stride;
-        launch_head(bx, B, ep, &fp);
+        launch_head(*bx, B, ep, &fp);
     }
 
     tdt::PrepArgs pa = prep_args(h, B);
@@ -424,7 +430,7 @@ int run_rows(HandleBox& bx, const TurboStepInputs* in, const TurboStepOutputs* o
         ep.no_sumexp = any_short ? 0u : 1u;  // greedy and full-vocabulary rows do not read them
         ep.ban = in->ban_bits;
         ep.ban_stride = in->ban_stride;
-        if (hidden) launch_head(bx, B, ep);
+        if (hidden) launch_head(*bx, B, ep);
         else tdt::launch_logits_epilogue(h, B, ep, h.stream);
     }
 
@@ -441,12 +447,22 @@ int run_rows(HandleBox& bx, const TurboStepInputs* in, const TurboStepOutputs* o
         sa.history = in->history;
         sa.hist_stride = in->history_stride;
         sa.hist_len = in->history_len;
+        sa.hist_overflow = h.overflow_dev;
     }
     tdt::launch_select(h, B, sa, any_fv, h.stream);
     return 1;
 }
 
-}  // namespace
+void set_last_error(const char* msg) { g_last_error = msg ? msg : ""; }
+
+int sample_on_head(Head& h, const TurboStepInputs* in, const TurboStepOutputs* out, float* logits) {
+    if (!logits) throw std::runtime_error("logits is NULL");
+    return run_rows(h, nullptr, in, out, nullptr, logits);
+}
+
+}  // namespace tdt
+
+using tdt::run_rows;
 
 #define API_TRY try {
 #define API_CATCH(ret)                                   \
@@ -603,6 +619,12 @@ TURBO_DT_API void* turbo_lmhead_create(const TurboLMHeadDesc* d) {
                   "map pinned ring");
         for (int i = 0; i < Head::kRing / Head::kRingGroup; ++i)
             check_hip(hipEventCreateWithFlags(&h.ring_ev[i], hipEventDisableTiming), "ring events");
+        check_hip(hipHostMalloc(reinterpret_cast<void**>(&h.overflow_host), sizeof(uint32_t),
+                                hipHostMallocMapped | hipHostMallocCoherent),
+                  "alloc history overflow word");
+        *h.overflow_host = 0u;
+        check_hip(hipHostGetDevicePointer(reinterpret_cast<void**>(&h.overflow_dev), h.overflow_host, 0),
+                  "map history overflow word");
         check_hip(hipDeviceSynchronize(), "create");
     } catch (...) {
         free_head(h);
@@ -638,6 +660,13 @@ TURBO_DT_API int turbo_lmhead_synchronize(void* handle) {
     Head& h = box(handle)->h;
     check_hip(hipSetDevice(h.device), "hipSetDevice");
     check_hip(hipStreamSynchronize(h.stream), "synchronize");
+    if (h.overflow_host && *h.overflow_host) {
+        const uint32_t row = *h.overflow_host - 1u;
+        *h.overflow_host = 0u;
+        throw std::runtime_error("history full: row " + std::to_string(row) +
+                                 "'s token was not appended (history_len reached history_stride); "
+                                 "later repetition/presence/frequency penalties would miss it");
+    }
     return 1;
     API_CATCH(0)
 }
@@ -696,7 +725,7 @@ TURBO_DT_API int turbo_lmhead_step(void* handle, const TurboStepInputs* in,
     HandleBox* bx = box(handle);
     check_hip(hipSetDevice(bx->h.device), "hipSetDevice");
     if (!in || !in->hidden) throw std::runtime_error("hidden is NULL");
-    return run_rows(*bx, in, out, in->hidden, nullptr);
+    return run_rows(bx->h, bx, in, out, in->hidden, nullptr);
     API_CATCH(0)
 }
 
@@ -707,7 +736,7 @@ TURBO_DT_API int turbo_sample_logits(void* handle, float* logits, const TurboSte
     HandleBox* bx = box(handle);
     check_hip(hipSetDevice(bx->h.device), "hipSetDevice");
     if (!logits) throw std::runtime_error("logits is NULL");
-    return run_rows(*bx, in, out, nullptr, logits);
+    return run_rows(bx->h, bx, in, out, nullptr, logits);
     API_CATCH(0)
 }
 

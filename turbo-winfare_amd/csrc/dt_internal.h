@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include "dt_common.h"
+#include "turbo_decode_tail.h"
 
 namespace tdt {
 
@@ -65,6 +66,10 @@ struct Head {
     // group: one event per kRingGroup steps marks the group's slots as read.
     static constexpr int kRing = 16;
     static constexpr int kRingGroup = 8;
+    // Set by the select kernel (row + 1) when TURBO_STEP_APPEND_HISTORY meets a full history;
+    // turbo_lmhead_synchronize reports and clears it. Pinned, mapped, coherent.
+    uint32_t* overflow_host = nullptr;
+    uint32_t* overflow_dev = nullptr;
     DevRow* ring_host = nullptr;       // [kRing][max_batch], pinned, mapped, coherent
     DevRow* ring_dev = nullptr;        // device-visible address of ring_host
     hipEvent_t ring_ev[kRing / kRingGroup] = {};
@@ -198,6 +203,7 @@ struct SelectArgs {
     uint32_t* history;            // append target or null
     uint32_t hist_stride;
     uint32_t* hist_len;
+    uint32_t* hist_overflow;      // host-mapped word set to (row + 1) when a full history drops a token, or null
     // multi-workgroup full-vocabulary path (null fv_acc: one workgroup per row)
     unsigned long long* fv_acc;     // [B][2][kFvBins] slice histograms summed by atomics
     unsigned long long* fv_merged;  // [B][2][kFvBins] merged histograms
@@ -210,6 +216,8 @@ constexpr uint32_t kFvSlices = 16;
 constexpr uint32_t kFvBins = 2048;
 constexpr uint32_t kFvCandCap = 8192;
 constexpr size_t kFvStateBytes = 128;
+// TurboRowReport.status bit: the row's history was full, so its token was not appended.
+constexpr uint32_t kStatusHistoryFull = 1u;
 // any_fv: some row takes the full-vocabulary value path (sampled, shortlist lifted).
 void launch_select(const Head& h, int batch, const SelectArgs& a, bool any_fv, hipStream_t st);
 
@@ -222,5 +230,12 @@ void launch_embed(const Head& h, const uint32_t* tokens, int n, float* out, floa
 
 // Throws std::runtime_error with the HIP error string on failure.
 void check_hip(hipError_t e, const char* what);
+
+// api.cpp: turbo_sample_logits on a head whose scratch the caller provides (h.Wt may be null: no
+// head kernel runs). Validates the rows and enqueues the modifier epilogue and the select on
+// h.stream; allocates nothing for batches of at most kInlineRows rows.
+int sample_on_head(Head& h, const TurboStepInputs* in, const TurboStepOutputs* out, float* logits);
+// api.cpp: sets the thread-local string turbo_lmhead_last_error returns.
+void set_last_error(const char* msg);
 
 }  // namespace tdt

@@ -60,6 +60,8 @@ struct RowReport {
     double total;
     double denom;
     double r;
+    uint32_t status;
+    uint32_t reserved;
 };
 
 struct SelShared {
@@ -739,17 +741,29 @@ __device__ inline RowCtx make_ctx(uint32_t V, const float* l, float m, float fmi
 
 // Row report and token, and the history append (src/runner.cpp:878), by thread 0. len: the
 // row's history length (read by the caller ahead of time), or ~0 to read it here.
+// A full history (len == stride) keeps its contents: the token is not appended, the report's
+// status carries kStatusHistoryFull and the host-visible overflow word (when given) is set, so
+// the caller's next synchronisation fails instead of the penalties silently drifting from a
+// history that grows without bound (src/runner.cpp:878).
 __device__ inline void write_row(const SelectArgs& a, uint32_t b, uint32_t token, const RowReport& rep,
                                  uint32_t len = 0xFFFFFFFFu) {
     if (threadIdx.x != 0) return;
     a.tokens[b] = token;
-    if (a.report) reinterpret_cast<RowReport*>(a.report)[b] = rep;
+    uint32_t status = 0u;
     if (a.history && a.hist_len && token != 0xFFFFFFFFu) {
         if (len == 0xFFFFFFFFu) len = a.hist_len[b];
         if (len < a.hist_stride) {
             a.history[(size_t)b * a.hist_stride + len] = token;
             a.hist_len[b] = len + 1u;
+        } else {
+            status |= kStatusHistoryFull;
+            if (a.hist_overflow) __hip_atomic_store(a.hist_overflow, b + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         }
+    }
+    if (a.report) {
+        RowReport r = rep;
+        r.status = status;
+        reinterpret_cast<RowReport*>(a.report)[b] = r;
     }
 }
 

@@ -21,6 +21,7 @@ TURBO_HIDDEN_F32 = 0
 TURBO_HIDDEN_BF16 = 1
 TURBO_STEP_NORMED = 1
 TURBO_STEP_APPEND_HISTORY = 2
+TURBO_STATUS_HISTORY_FULL = 1
 
 # Every symbol include/turbo_decode_tail.h declares.
 EXPORTS = (
@@ -116,6 +117,8 @@ class TurboRowReport(C.Structure):
         ("total", C.c_double),
         ("denom", C.c_double),
         ("r", C.c_double),
+        ("status", C.c_uint32),
+        ("reserved", C.c_uint32),
     ]
 
 
