@@ -294,6 +294,29 @@ TURBO_DT_API int turbo_apply_repetition_penalty(void* hip_stream, float* logits,
 TURBO_DT_API int turbo_sample_logits(void* handle, float* logits, const TurboStepInputs* in,
                                      const TurboStepOutputs* out);
 
+/* ---- sampling without a handle or an allocation ---------------------------------------- */
+
+#define TURBO_NOALLOC_MAX_BATCH 4
+#define TURBO_NOALLOC_MAX_VOCAB 262144
+
+/*
+ * turbo_sample_logits without a handle and without allocating: the modifiers of
+ * TurboStepInputs and the sampler (sample_token semantics, src/sampling.cpp:92-169) over
+ * caller logits [batch][vocab], modified in place, tokens (and reports) into `out`. No
+ * counterpart in the reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It calls no hipMalloc,
+ * hipFree or allocating routine; its working memory is one static device array of about 14 MiB
+ * per GPU (held until the process ends), sized for batch <= TURBO_NOALLOC_MAX_BATCH and
+ * vocab <= TURBO_NOALLOC_MAX_VOCAB, with at most 8192 logit-bias entries per row. Larger inputs
+ * fail with a clear error. The work is enqueued on hip_stream (NULL = the null stream) of the
+ * current device; the first call on a device clears the array on that stream. Every call on a GPU
+ * shares that GPU's array: calls that overlap on one GPU race, so the caller serialises them.
+ * in->hidden and out->logits are ignored; TURBO_STATUS_HISTORY_FULL is reported per row only.
+ */
+TURBO_DT_API int turbo_sample_logits_noalloc(void* hip_stream, uint32_t vocab, float final_logit_softcap,
+                                             float* logits, const TurboStepInputs* in,
+                                             const TurboStepOutputs* out);
+
 /* ---- measurement ------------------------------------------------------------------------- */
 
 /* When enabled, the head kernel (the int4 GEMV / MFMA kernel) is launched with HIP start and

@@ -17,7 +17,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
 LIB = PKG / "lib" / "libturbo_decode_tail.so"
-SOURCES = ["api.cpp", "bundle.cpp", "prep.hip", "gemv_digits.hip", "gemm_mfma.hip", "select.hip", "misc.hip"]
+SOURCES = ["api.cpp", "bundle.cpp", "prep.hip", "gemv_digits.hip", "gemm_mfma.hip", "select.hip", "misc.hip", "noalloc.hip"]
 ARCH = "gfx950"
 FLAGS = [
     f"--offload-arch={ARCH}",

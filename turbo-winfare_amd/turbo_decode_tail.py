@@ -51,7 +51,11 @@ EXPORTS = (
     "turbo_bundle_decode_header",
     "turbo_bundle_find_tensor",
     "turbo_lmhead_create_from_bundle",
+    "turbo_sample_logits_noalloc",
 )
+
+TURBO_NOALLOC_MAX_BATCH = 4
+TURBO_NOALLOC_MAX_VOCAB = 262144
 
 
 class TurboLMHeadDesc(C.Structure):
@@ -189,6 +193,8 @@ def load(path: os.PathLike | str | None = None) -> C.CDLL:
         "turbo_bundle_decode_header": (i32, [vp, C.c_size_t, C.POINTER(C.c_uint64)]),
         "turbo_bundle_find_tensor": (i32, [C.c_char_p, C.c_char_p, C.POINTER(TurboBundleTensor)]),
         "turbo_lmhead_create_from_bundle": (vp, [C.c_char_p, f32, f32, i32]),
+        "turbo_sample_logits_noalloc": (i32, [vp, u32, f32, vp, C.POINTER(TurboStepInputs),
+                                              C.POINTER(TurboStepOutputs)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -369,6 +375,13 @@ class LMHead:
         ms, n = C.c_double(), C.c_int()
         _ok(self.lib.turbo_lmhead_head_kernel_time(self.h, C.byref(ms), C.byref(n), 1 if reset else 0))
         return ms.value, n.value
+
+
+def sample_logits_noalloc(logits, vocab: int, inp: TurboStepInputs, tokens, report=None, *,
+                          softcap: float = 30.0, stream=None) -> None:
+    """turbo_sample_logits_noalloc: the sampler over caller logits with no handle (static scratch)."""
+    out = TurboStepOutputs(_ptr(tokens), None, _ptr(report))
+    _ok(load().turbo_sample_logits_noalloc(stream, vocab, softcap, _ptr(logits), C.byref(inp), C.byref(out)))
 
 
 def softcap(z, n: int, cap: float, stream=None) -> None:
