@@ -293,6 +293,28 @@ def widened_lines(T, torch):
                                            "kernel_GBs": byts / (kus * 1e-6) / 1e9,
                                            "algorithmic_bytes": byts}
         h.close()
+    # the 8 routed experts of one token: gate + up (16 x 704 x 2816, one input row) in one grouped
+    # launch, then the 8 down matrices (2816 x 704) in another; against one call per matrix
+    out["experts_grouped"] = {}
+    for name, shape, n in (("gate_up_16x704x2816", (704, 2816), 16), ("down_8x2816x704", (2816, 704), 8)):
+        rows, k = shape
+        mats, heads = [], []
+        for i in range(n):
+            W, S, B, _ = synth.make_head(rows, k, 3000 + i)
+            m = T.Int4Matrix(rows, k)
+            m.load_weights(W, S, B)
+            mats.append(m)
+        xs = [torch.from_numpy(synth.hidden_states(1, k, 80 + i)[0]).cuda() for i in range(n)]
+        outs = [torch.empty(rows, dtype=torch.float32, device="cuda") for _ in range(n)]
+        for _ in range(20):
+            T.matvec_grouped(mats, xs, outs)
+        reps = 200
+        el = time_loop(torch, lambda s: T.matvec_grouped(mats, xs, outs), 0, reps)
+        byts = n * (rows * k // 2 + rows * (k // 64) * 4 + k * 4 + rows * 4)
+        out["experts_grouped"][name] = {"call_us": 1e6 * el / reps, "matrices": n, "algorithmic_bytes": byts,
+                                        "GBs": byts / (el / reps) / 1e9}
+        for m in mats:
+            m.close()
     W, S, B, g = synth.make_head(V, D, SEED)
     h = T.LMHead(W, S, B, g, vocab=V, hidden=D)
     for ntok in (1, 256):

@@ -253,6 +253,32 @@ TURBO_DT_API int turbo_lmhead_step(void* handle, const TurboStepInputs* in,
 TURBO_DT_API int turbo_int4_matvec(void* handle, const void* x, int x_dtype, int batch, float* out);
 
 /*
+ * ---- int4 matrices of the layer loop ------------------------------------------------------
+ * A matrix handle holds one affine-int4 weight matrix (rows x in_dim, group 64, BF16 scale +
+ * bias; the reference layout of turbo_lmhead_create) in the kernels' tiled layout and nothing
+ * else, so its device footprint is the table's size (rows * in_dim / 2 + rows * in_dim / 16
+ * bytes). These replace the GemvInt4 dispatches of the layer loop (shaders/GemvInt4.hlsl:1-38;
+ * src/runner.cpp:431-442, :612-646, :671-678) for the expert slots and projections.
+ */
+/* rows 1..16777216, in_dim a multiple of 64 up to 8192. Allocates the table only; the contents
+ * are undefined until turbo_int4_matrix_load. NULL on failure. */
+TURBO_DT_API void* turbo_int4_matrix_create(uint32_t rows, uint32_t in_dim, int device);
+/* Repacks one matrix into the handle (the expert streamer's slot refill, src/streamer.cpp:171-214).
+ * weights_on_device = 1: the three pointers are device memory (for example the slot's buffer at
+ * the tensor's offsets); the repack is one kernel pair enqueued on hip_stream, allocating nothing.
+ * 0: host memory, staged through temporary device buffers and finished before the call returns. */
+TURBO_DT_API int turbo_int4_matrix_load(void* matrix, const uint8_t* weight, const uint16_t* scales,
+                                        const uint16_t* biases, int weights_on_device, void* hip_stream);
+TURBO_DT_API void turbo_int4_matrix_destroy(void* matrix);
+/* out[i][r] = sum_c (q[r][c] * scale + bias) * x[i][c] for each of `count` (0..32) matrices of one
+ * device, in one kernel launch on hip_stream: for example the 8 routed experts' gate and up
+ * matrices of a token (16 products of 704 x 2816), then their down matrices. x[i]: [in_dim] FP32,
+ * 16-byte aligned; out[i]: [rows] FP32; all device memory. Each out[i] is bit-identical to
+ * turbo_int4_matvec on a head of the same matrix. */
+TURBO_DT_API int turbo_int4_matvec_grouped(void* const* matrices, int count, const float* const* x,
+                                           float* const* out, void* hip_stream);
+
+/*
  * Embedding lookup on the same tied table (shaders/EmbedLookup.hlsl:1-45; CPU
  * src/cpu_reference.cpp:108-124 and :323-329): out[i] = row tokens[i] dequantised as
  * (float)q * scale + bias, times sqrtf(hidden). tokens: [n] device ids, out: [n][hidden] FP32

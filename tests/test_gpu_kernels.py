@@ -153,3 +153,28 @@ def test_repetition_penalty_kernel():
         want = l.copy()
         O.orc().orc_apply_repetition_penalty(want, V, hist.ctypes.data if n else None, n, p, 30.0)
         assert np.array_equal(t.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("batch", [3, 64])
+def test_logits_mfma_path_large_scales(batch):
+    """The batched head's fp16 dequant has two forms: nibbles as fp16 denormals times s * 2^20
+    (every |s| < 1/16) and nibbles through the mantissa of 1024.0 (any scale). A head whose group
+    scales reach past 1/16 (the synthetic scales times 16, so the largest are ~0.3) takes the
+    second form on every batched kernel, with the same tolerance."""
+    Vh = 8192
+    W, S, B, g = synth.make_head(Vh, D, 103)
+    S = synth.f32_to_bf16(synth.bf16_to_f32(S) * 16.0)
+    B = synth.f32_to_bf16(synth.bf16_to_f32(B) * 16.0)  # the same q - 8 centring
+    assert float(synth.bf16_to_f32(S).max()) > 1.0 / 16
+    h = T.LMHead(W, S, B, g, vocab=Vh, hidden=D)
+    try:
+        x = np.stack([O.rms_norm(r, g, 1e-6) for r in synth.hidden_states(batch, D, 8)])
+        out = torch.empty((batch, Vh), dtype=torch.float32, device="cuda")
+        h.logits(dev(x), batch, out)
+        h.sync()
+        got = out.cpu().numpy()
+        for b in sorted({0, batch // 2, batch - 1}):
+            want = O.softcap(O.matvec(W, S, B, x[b], U.THREADS), 30.0)
+            assert U.logit_err(got[b], want) <= U.LOGIT_RTOL, b
+    finally:
+        h.close()

@@ -116,3 +116,73 @@ def test_folded_logits_big_head_matches_prepared():
             assert t1.cpu().tolist() == want and t2.cpu().tolist() == want, batch
     finally:
         h.close()
+
+
+def test_grouped_matvec_matches_head_calls():
+    """turbo_int4_matvec_grouped: the 8 routed experts' gate and up matrices (16 x 704 x 2816)
+    with one input row, then their 8 down matrices (2816 x 704) each with its own row, in one
+    launch each, from matrix handles that hold only the tables. Every output must equal the
+    same matrix's turbo_int4_matvec through a head bit for bit, and the oracle to the reference's
+    tolerance. One matrix is loaded from device memory (the slot-refill path), the rest from host
+    arrays; a second load replaces a matrix's contents."""
+    rng_mats = []
+    for e in range(8):
+        for kind, (rows, k) in (("gate", (704, 2816)), ("up", (704, 2816))):
+            rng_mats.append((rows, k, 1000 + 2 * e + (kind == "up")))
+    downs = [(2816, 704, 2000 + e) for e in range(8)]
+    for group, shared_x in ((rng_mats, True), (downs, False)):
+        mats, tables = [], []
+        for i, (rows, k, seed) in enumerate(group):
+            W, S, B, _ = synth.make_head(rows, k, seed)
+            m = T.Int4Matrix(rows, k)
+            if i == 0:
+                m.load_weights(torch.from_numpy(W).cuda(), torch.from_numpy(S.view(np.int16)).cuda(),
+                               torch.from_numpy(B.view(np.int16)).cuda(), on_device=True)
+            else:
+                m.load_weights(W, S, B)
+            mats.append(m)
+            tables.append((W, S, B))
+        k = group[0][1]
+        xs_np = [synth.hidden_states(1, k, 70 + (0 if shared_x else i))[0] for i in range(len(group))]
+        xs = [torch.from_numpy(x).cuda() for x in xs_np]
+        outs = [torch.full((r,), float("nan"), dtype=torch.float32, device="cuda") for r, _, _ in group]
+        T.matvec_grouped(mats, xs, outs)
+        torch.cuda.synchronize()
+        for i, (rows, kk, seed) in enumerate(group):
+            W, S, B = tables[i]
+            got = outs[i].cpu().numpy()
+            want = O.matvec(W, S, B, xs_np[i], U.THREADS)
+            assert np.all(np.abs(got - want) <= 1e-5 + 1e-4 * np.abs(want)), i
+            h = T.LMHead(W, S, B, None, vocab=rows, hidden=kk, softcap=0.0)
+            try:
+                ref = torch.empty((1, rows), dtype=torch.float32, device="cuda")
+                h.matvec(xs[i].view(1, kk), 1, ref)
+                h.sync()
+                assert np.array_equal(got.view(np.uint32), ref.cpu().numpy()[0].view(np.uint32)), i
+            finally:
+                h.close()
+        # reload one matrix with another table: the next call uses the new contents
+        W2, S2, B2, _ = synth.make_head(group[1][0], group[1][1], 999)
+        mats[1].load_weights(W2, S2, B2)
+        T.matvec_grouped(mats[:2], xs[:2], outs[:2])
+        torch.cuda.synchronize()
+        want = O.matvec(W2, S2, B2, xs_np[1], U.THREADS)
+        assert np.all(np.abs(outs[1].cpu().numpy() - want) <= 1e-5 + 1e-4 * np.abs(want))
+        for m in mats:
+            m.close()
+
+
+def test_grouped_matvec_rejects_bad_calls():
+    m = T.Int4Matrix(64, 128)
+    try:
+        x = torch.zeros(128, dtype=torch.float32, device="cuda")
+        o = torch.zeros(64, dtype=torch.float32, device="cuda")
+        with pytest.raises(T.TurboError, match="count must be in"):
+            T.matvec_grouped([m] * 33, [x] * 33, [o] * 33)
+        with pytest.raises(T.TurboError, match="16-byte aligned"):
+            T.matvec_grouped([m], [x.data_ptr() + 4], [o])
+        T.matvec_grouped([], [], [])  # nothing to do
+    finally:
+        m.close()
+    with pytest.raises(T.TurboError, match="in_dim must be"):
+        T.Int4Matrix(64, 100)

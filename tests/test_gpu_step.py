@@ -79,15 +79,21 @@ def test_config1_greedy_b1(head):
 
 
 def test_config2_sampled_b1_with_history(head):
+    """Config 2 over 128 consecutive decode steps (the reference's token-for-token gate,
+    CONTRIBUTING.md:37-47, on the sampled path): each step's logits against the oracle chain and
+    its token against the oracle's, the history growing on the device by each GPU token. The
+    replay is teacher-forced on the GPU's tokens, so a near-tie (counted) does not cascade."""
     h, (W, S, B, g) = head
+    steps = 128
     hist0 = synth.uniform_ids(256, V, SEED)
-    cap = 256 + 16
+    cap = 256 + steps
     hist = torch.zeros((1, cap), dtype=torch.int32, device="cuda")
     hist[0, :256] = torch.from_numpy(hist0.astype(np.int32))
     hlen = torch.tensor([256], dtype=torch.int32, device="cuda")
     host_hist = list(hist0)
     mism = 0
-    for step in range(6):
+    worst = 0.0
+    for step in range(steps):
         x = synth.hidden_states(1, D, SEED + 1, step)
         r = T.row_default(temperature=0.8, top_k=64, top_p=0.95, repetition_penalty=1.1,
                           seed=SEED, counter=step)
@@ -97,15 +103,18 @@ def test_config2_sampled_b1_with_history(head):
                                 history=hist, history_len=hlen)
         want_l, info = U.oracle_row(W, S, B, g, x[0], oparams(r), u,
                                     history=np.array(host_hist, np.uint32))
-        assert U.logit_err(logits[0], want_l) <= 1e-4
+        err = U.logit_err(logits[0], want_l)
+        worst = max(worst, err)
+        assert err <= 1e-4, (step, err)
         check_sampler_on_gpu_logits([r], toks, logits, [u])
         if int(toks[0]) != info.token:
-            assert U.sample_near_tie(info, want_l, oparams(r))
+            assert U.sample_near_tie(info, want_l, oparams(r)), step
             mism += 1
         host_hist.append(int(toks[0]))
-        assert int(hlen.item()) == 257 + step
-        assert int(hist[0, 256 + step].item()) == int(toks[0])
-    assert mism <= 1
+    assert int(hlen.item()) == 256 + steps
+    assert np.array_equal(hist.cpu().numpy()[0, 256:].astype(np.uint32), np.array(host_hist[256:], np.uint32))
+    print(f"config2: {steps} steps, {mism} near-tie token mismatches, worst logit error {worst:.2e}")
+    assert mism <= max(1, steps // 32)
 
 
 def test_config3_mixed_b32(head):
@@ -149,10 +158,18 @@ def test_config4_b256_full_vocab_nucleus(head):
         info = O.sample(logits[b], p, us[b])
         if int(toks[b]) != info.token:
             assert U.sample_near_tie(info, logits[b], p), b
-    for b in (0, 255):
+    # eight rows through the whole oracle chain: oracle logits, then the oracle sampler
+    near = 0
+    for b in (0, 37, 74, 111, 148, 185, 222, 255):
         xf = synth.bf16_to_f32(xb[b])
         want_l = O.softcap(O.matvec(W, S, B, xf, U.THREADS), 30.0)
         assert U.logit_err(logits[b], want_l) <= U.LOGIT_RTOL
+        p = oparams(rows[b])
+        info = O.sample(want_l, p, us[b])
+        if int(toks[b]) != info.token:
+            assert U.sample_near_tie(info, want_l, p), b
+            near += 1
+    print(f"config4: 8 rows through the oracle chain, {near} near-tie token mismatches")
 
 
 def test_b256_logits_equal_b32_logits(head):

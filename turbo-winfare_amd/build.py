@@ -17,7 +17,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
 LIB = PKG / "lib" / "libturbo_decode_tail.so"
-SOURCES = ["api.cpp", "bundle.cpp", "prep.hip", "gemv_digits.hip", "gemm_mfma.hip", "select.hip", "misc.hip", "noalloc.hip"]
+SOURCES = ["api.cpp", "bundle.cpp", "prep.hip", "gemv_digits.hip", "gemm_mfma.hip", "select.hip", "misc.hip", "noalloc.hip", "matrix.cpp"]
 ARCH = "gfx950"
 FLAGS = [
     f"--offload-arch={ARCH}",
@@ -58,7 +58,8 @@ def build(verbose: bool = False) -> Path:
     with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 4)) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", f"-Wl,-soname,{LIB.name}", "-o", str(tmp),
+           *map(str, objs)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")

@@ -40,6 +40,7 @@ void clear_error() { g_last_error.clear(); }
 
 constexpr int kMaxBatch = 256;
 
+
 struct HandleBox {
     uint32_t magic = 0x54445448u;  // "TDTH"
     Head h;
@@ -147,6 +148,7 @@ void free_head(Head& h) {
     dfree(h.xws);
     dfree(h.xsum);
     dfree(h.x16);
+    dfree(h.SB16t);
     dfree(h.logits);
     dfree(h.partials);
     dfree(h.rows);
@@ -208,6 +210,7 @@ tdt::PrepArgs prep_args(const Head& h, int B) {
     a.xws = h.xws;
     a.xsum = h.xsum;
     a.x16 = h.x16;
+    a.x16_denorm = h.mfma_denorm ? 1 : 0;
     a.V = h.V;
     a.ntile = h.ntile;
     a.P = 2;
@@ -555,6 +558,7 @@ TURBO_DT_API void* turbo_lmhead_create(const TurboLMHeadDesc* d) {
         const size_t gcount = static_cast<size_t>(h.V) * h.G;
         h.Wt = dalloc<uint4>(static_cast<size_t>(h.ntile) * h.NC * tdt::kTileRows, "alloc Wt");
         h.SBt = dalloc<uint32_t>(static_cast<size_t>(h.ntile) * h.G * tdt::kTileRows, "alloc SBt");
+        h.SB16t = dalloc<uint32_t>(static_cast<size_t>(h.ntile) * h.G * tdt::kTileRows, "alloc SB16t");
 
         const uint8_t* W = d->weight;
         const uint16_t* S = d->scales;
@@ -573,8 +577,7 @@ TURBO_DT_API void* turbo_lmhead_create(const TurboLMHeadDesc* d) {
             S = tS;
             Bi = tB;
         }
-        tdt::launch_repack(h, W, S, Bi, nullptr);
-        check_hip(hipDeviceSynchronize(), "repack");
+        h.mfma_denorm = tdt::launch_repack(h, W, S, Bi, nullptr);
         dfree(tW);
         dfree(tS);
         dfree(tB);

@@ -33,6 +33,11 @@ struct Head {
     // (scale bf16 | bias bf16 << 16).
     uint4* Wt = nullptr;
     uint32_t* SBt = nullptr;
+    // Matrix-core form of the scales and biases: SB16t[tile][group][64 rows] u32 = fp16(s) * 2^20 |
+    // fp16(b) << 16 when mfma_denorm (every |s| < 1/16: the dequant multiplies nibbles held as fp16
+    // denormals), else fp16(s) | fp16(b) << 16 (the dequant through the mantissa of 1024.0).
+    uint32_t* SB16t = nullptr;
+    bool mfma_denorm = true;
     uint16_t* gamma = nullptr;   // [D] bf16 or null
 
     int max_batch = 0;
@@ -129,6 +134,7 @@ struct PrepArgs {
     float* xws;
     float* xsum;
     uint16_t* x16;
+    int x16_denorm;              // fp16 layout: (16 x, x) per (even, odd) element, else (x, x / 16)
     // history counts and the bias table
     uint32_t V, ntile, P;        // P: bias sort size (power of two >= bias_stride)
     uint32_t* hcount;
@@ -148,7 +154,9 @@ struct PrepArgs {
     uint32_t mod_bits[16];       // 2 bits per row (DevRow::has_mods), so no block reads the
                                  // host-mapped staging slot except the row copy
 };
-void launch_repack(const Head& h, const uint8_t* W, const uint16_t* S, const uint16_t* B,
+// Fills Wt, SBt and SB16t; returns whether every scale fits the denormal dequant (|s| < 1/16),
+// in which case SB16t holds s * 2^20, else s (synchronises).
+bool launch_repack(const Head& h, const uint8_t* W, const uint16_t* S, const uint16_t* B,
                    hipStream_t st);
 void launch_step_prep(const Head& h, const PrepArgs& a, bool with_mods, hipStream_t st);
 uint32_t modtable_sort_size(const Head& h, uint32_t n);
@@ -179,6 +187,28 @@ void launch_head_digits_fused(const Head& h, int batch, const FusedPrep& fp, con
                               hipStream_t st, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
 // Threads per workgroup of the split digit kernel for this head (0: one wave per tile instead).
 uint32_t split_threads(const Head& h);
+// Waves the split digit kernel gives one 64-row tile of a G-group matrix with ntile tiles.
+uint32_t split_waves(uint32_t G, uint32_t ntile);
+
+// Grouped matrix-vector products (one input row per matrix, raw fp32 outputs), one launch.
+constexpr uint32_t kMaxGroupMats = 32;
+struct GroupMat {
+    const uint4* Wt;
+    const uint32_t* SBt;
+    const float* x;      // [D] fp32 device
+    float* out;          // [rows] fp32 device
+    uint32_t rows, D;
+    uint32_t tile_begin; // first workgroup of this matrix
+    uint32_t ks;         // waves per tile (split_waves), at least 1
+};
+struct GroupArgs {
+    GroupMat m[kMaxGroupMats];
+    uint32_t count;
+};
+void launch_matvec_grouped(const GroupArgs& a, uint32_t total_tiles, hipStream_t st);
+// prep.hip: the tiled table of any matrix (Wt [ntile][NC][64] x 16 B, SBt [ntile][G][64] u32).
+void launch_repack_table(uint4* Wt, uint32_t* SBt, uint32_t V, uint32_t NC, uint32_t G, uint32_t ntile,
+                         const uint8_t* W, const uint16_t* S, const uint16_t* B, hipStream_t st);
 
 // gemv_digits.hip / gemm_mfma.hip
 // ev0 / ev1 (may be null): timing events stamped by the head kernel's own dispatch

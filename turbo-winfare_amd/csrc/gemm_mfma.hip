@@ -4,14 +4,10 @@
 //
 // Design (gfx950):
 //  * v_mfma_f32_32x32x16_f16: A = dequantised weights (32 vocabulary rows), B = activations
-//    (32 batch rows), fp32 accumulation. Weights are dequantised once per wave in registers:
-//    a nibble becomes an exact fp16 through the 0x6400 exponent trick and one v_pk_add_f16,
-//    then one v_pk_fma_f16 applies scale and bias, rounding once to fp16 (relative error
-//    <= 2^-11; bf16 would be 2^-8 at the same MFMA rate).
-//  * High nibbles are extracted in place (w & 0x00F000F0 gives 16 q), so their halves hold
-//    16 * round16(q s + b) (bias pre-multiplied by 16) and the matching activation slots hold
-//    x / 16. Power-of-two scaling commutes with rounding, so every product is exactly the
-//    intended w * x while the dequant costs 13 VALU ops per 8 weights.
+//    (32 batch rows), fp32 accumulation. Weights are dequantised once per wave in registers
+//    (dequant_word, dt_mfma.h): q s + b rounded once to fp16 (relative error <= 2^-11; bf16
+//    would be 2^-8 at the same MFMA rate), from nibbles masked into fp16 denormals when every
+//    scale is below 1/16 (9 VALU ops per 8 weights), else through the mantissa of 1024.0 (13).
 //  * Per 64-k group a lane loads one 16-byte chunk per 32-row fragment: lanes 0-31 the chunk
 //    2g of rows 0-31, lanes 32-63 the chunk 2g+1 of the same rows (two contiguous 512-byte
 //    runs of the tiled layout). MFMA step j consumes word j of the lane's chunk; the
@@ -30,75 +26,9 @@
 #include <stdexcept>
 #include <utility>
 
-#include "dt_epilogue.h"
+#include "dt_mfma.h"
 
 namespace tdt {
-
-typedef _Float16 h2v __attribute__((ext_vector_type(2)));
-typedef _Float16 h8v __attribute__((ext_vector_type(8)));
-typedef float f16v __attribute__((ext_vector_type(16)));
-
-constexpr uint32_t kColHalves = 72;  // 64 halves of a group + 8 padding (LDS bank spread)
-
-__device__ inline h2v as_h2(uint32_t u) { return __builtin_bit_cast(h2v, u); }
-
-typedef unsigned v4u __attribute__((ext_vector_type(4)));
-
-// The table is streamed once per step (nontemporal: it does not displace the activations).
-__device__ inline uint4 load_stream(const uint4* p) {
-    const v4u t = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
-    return make_uint4(t.x, t.y, t.z, t.w);
-}
-__device__ inline uint32_t load_stream(const uint32_t* p) { return __builtin_nontemporal_load(p); }
-
-// 8 nibbles -> 8 halves (e0, e4, 16e1', 16e5', e2, e6, 16e3', 16e7') where e' = q s + b and the
-// primed slots carry the factor 16 (bias b16 = 16 b).
-__device__ inline h8v dequant_word(uint32_t w, h2v s2, h2v b2, h2v b16) {
-    const uint32_t magic = 0x64006400u;  // fp16 1024.0 in both halves
-    const h2v off = as_h2(magic);
-    const uint32_t w8 = w >> 8;
-    const h2v q0 = as_h2((w & 0x000F000Fu) | magic) - off;   // (e0, e4)
-    const h2v q1 = as_h2((w & 0x00F000F0u) | magic) - off;   // (16 e1, 16 e5)
-    const h2v q2 = as_h2((w8 & 0x000F000Fu) | magic) - off;  // (e2, e6)
-    const h2v q3 = as_h2((w8 & 0x00F000F0u) | magic) - off;  // (16 e3, 16 e7)
-    const h2v r0 = __builtin_elementwise_fma(q0, s2, b2);
-    const h2v r1 = __builtin_elementwise_fma(q1, s2, b16);
-    const h2v r2 = __builtin_elementwise_fma(q2, s2, b2);
-    const h2v r3 = __builtin_elementwise_fma(q3, s2, b16);
-    h8v o;
-    o[0] = r0[0]; o[1] = r0[1]; o[2] = r1[0]; o[3] = r1[1];
-    o[4] = r2[0]; o[5] = r2[1]; o[6] = r3[0]; o[7] = r3[1];
-    return o;
-}
-
-// Softcap for the batched path: x = z / cap through the reciprocal, then
-// tanh(x) = sign(x) (1 - 2 / (exp(2|x|) + 1)) with the hardware exp2 and rcp. For large |x|
-// exp overflows to +inf and rcp(inf) = 0 gives exactly +-1, as libm's tanhf does once
-// |x| > 9. Relative error ~1e-6, far below this path's fp16-dequant error.
-__device__ inline float softcap_fast(float z, float cap, float inv_cap) {
-    const float x = z * inv_cap;
-    const float e = __builtin_amdgcn_exp2f(fabsf(x) * 2.8853900817779268f);  // exp(2|x|)
-    const float t = fmaf(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f);
-    return cap * copysignf(t, x);
-}
-
-// Row held in register r of a 32x32 accumulator by a lane with half hl (0/1): 8(r/4) + 4hl + r%4.
-__device__ inline uint32_t acc_row(int r, uint32_t hl) { return 8u * (uint32_t)(r >> 2) + 4u * hl + (uint32_t)(r & 3); }
-
-// Scale / bias halves of one (row, group): s, b and 16 b (for the high-nibble slots).
-struct SbHalves {
-    h2v s2, b2, b16;
-};
-__device__ inline SbHalves unpack_sb(uint32_t sc) {
-    const _Float16 sh = (_Float16)bf16_to_f32(sc & 0xFFFFu);
-    const float bf = bf16_to_f32(sc >> 16);
-    SbHalves r;
-    r.s2 = h2v{sh, sh};
-    r.b2 = h2v{(_Float16)bf, (_Float16)bf};
-    r.b16 = h2v{(_Float16)(16.0f * bf), (_Float16)(16.0f * bf)};
-    return r;
-}
-__device__ inline uint32_t word_of(const uint4& w, int j) { return (j == 0) ? w.x : (j == 1) ? w.y : (j == 2) ? w.z : w.w; }
 
 // Workgroup = 4 waves, one 64-row tile each, over a block of NCOL = 32 NB batch columns
 // (the column block). Two or more independent workgroups share a CU, so one's epilogue overlaps
@@ -108,10 +38,10 @@ __device__ inline uint32_t word_of(const uint4& w, int j) { return (j == 0) ? w.
 // last group are clamped to it and never used, so the compiler's load counters stay exact and
 // the weight prefetch is never drained early. The next k-step's weights are dequantised in
 // the shadow of the current step's MFMAs.
-template <int NB, int PF, int OCC, bool FULL>
+template <int NB, int PF, int OCC, bool FULL, bool DENORM>
 __global__ __launch_bounds__(256, OCC) void k_head_mfma(
-    const uint4* __restrict__ Wt, const uint32_t* __restrict__ SBt, const uint16_t* __restrict__ x16,
-    uint32_t B, uint32_t D, uint32_t NC, uint32_t G, uint32_t ncb, uint32_t ntg, EpiArgs ep) {
+    const uint4* __restrict__ Wt, const uint32_t* __restrict__ SB16t,
+    const uint16_t* __restrict__ x16, uint32_t B, uint32_t D, uint32_t NC, uint32_t G, uint32_t ncb, uint32_t ntg, EpiArgs ep) {
     constexpr uint32_t NT = 256;
     constexpr uint32_t NCOL = 32 * NB;
     constexpr uint32_t XP = NCOL * 8;                 // 16-byte activation pieces per group
@@ -133,9 +63,10 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
     const uint32_t hl = lane >> 5, l32 = lane & 31u;
 
     const uint4* wbase = Wt + (size_t)tile * NC * kTileRows + (size_t)hl * kTileRows + l32;
-    const uint32_t* sbbase = SBt + (size_t)tile * G * kTileRows + l32;
-    auto wload = [&](uint32_t g, int mb) { return load_stream(wbase + (size_t)(2u * g) * kTileRows + 32u * mb); };
-    auto sload = [&](uint32_t g, int mb) { return load_stream(sbbase + (size_t)g * kTileRows + 32u * mb); };
+    const uint32_t* sbbase = SB16t + (size_t)tile * G * kTileRows + l32;
+    auto wload = [&](uint32_t g, int mb) { return mfma_load_stream(wbase + (size_t)(2u * g) * kTileRows + 32u * mb); };
+    auto sload = [&](uint32_t g, int mb) { return mfma_load_stream(sbbase + (size_t)g * kTileRows + 32u * mb); };
+    const uint32_t magic = DENORM ? 0u : magic_vgpr();
 
     auto load_x = [&](uint32_t g, v4u* xr) {
 #pragma unroll
@@ -186,8 +117,8 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
     h8v acur[2], anext[2];
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
-        const SbHalves h = unpack_sb(sbr[0][mb]);
-        acur[mb] = dequant_word(wr[0][mb].x, h.s2, h.b2, h.b16);
+        const SbHalves h = unpack_sb16<DENORM>(sbr[0][mb]);
+        acur[mb] = dequant_word<DENORM>(wr[0][mb].x, h.s2, h.b2, h.bx, magic);
     }
     uint32_t buf = 0;
     for (uint32_t g0 = 0; g0 < G; g0 += PF) {
@@ -197,7 +128,7 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
             uint4 wc[2];
             SbHalves hc[2];
 #pragma unroll
-            for (int mb = 0; mb < 2; ++mb) { wc[mb] = wr[p][mb]; hc[mb] = unpack_sb(sbr[p][mb]); }
+            for (int mb = 0; mb < 2; ++mb) { wc[mb] = wr[p][mb]; hc[mb] = unpack_sb16<DENORM>(sbr[p][mb]); }
             // slot p held group g, whose activations are already in LDS: refill it with g + PF
             const uint32_t gn = min(g + (uint32_t)PF, G - 1u);
 #pragma unroll
@@ -219,10 +150,10 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
 #pragma unroll
                 for (int mb = 0; mb < 2; ++mb) {
                     if (j < 3) {
-                        anext[mb] = dequant_word(word_of(wc[mb], j + 1), hc[mb].s2, hc[mb].b2, hc[mb].b16);
+                        anext[mb] = dequant_word<DENORM>(word_of(wc[mb], j + 1), hc[mb].s2, hc[mb].b2, hc[mb].bx, magic);
                     } else {
-                        const SbHalves h = unpack_sb(sbr[pn][mb]);
-                        anext[mb] = dequant_word(wr[pn][mb].x, h.s2, h.b2, h.b16);
+                        const SbHalves h = unpack_sb16<DENORM>(sbr[pn][mb]);
+                        anext[mb] = dequant_word<DENORM>(wr[pn][mb].x, h.s2, h.b2, h.bx, magic);
                     }
                 }
 #pragma unroll
@@ -258,13 +189,13 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
     if (!tile_ok) return;
 
     // ---- epilogue, in place on the accumulators ----
-    // The transposed logit stores reuse the activation buffer: one 32 x kTrRow float tile per
-    // wave (rows padded to spread the LDS banks), after every wave's last read of it (the main
-    // loop ends with a barrier).
-    constexpr uint32_t kTrRow = 68;
+    // The transposed logit stores (four column blocks) reuse the activation buffer: one
+    // 32 x kTrRow float tile per wave, after every wave's last read of it (the main loop ends
+    // with a barrier).
     constexpr bool kTransposeStores = NB == 4;
     static_assert(!kTransposeStores || sizeof(lx) >= 4u * 32u * kTrRow * sizeof(float),
                   "four wave tiles must fit the activation buffer");
+    float* epi_tl = reinterpret_cast<float*>(&lx[0][0]) + wave * (32u * kTrRow);
     const uint32_t base = tile * kTileRows;
     const bool vec_ok = (ep.V & 3u) == 0u;  // float4 stores need 16-byte aligned rows
     const bool full_tile = base + kTileRows <= ep.V;
@@ -362,7 +293,7 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
         // one float4 store covers four whole 256-byte row segments instead of 16 bytes of 32
         // rows. Otherwise (and for partial tiles or columns) the values leave as they lie.
         if (kTransposeStores && ep.logits && full_tile && vec_ok && cbase + 32u * nb + 32u <= B) {
-            float* tl = reinterpret_cast<float*>(&lx[0][0]) + wave * (32u * kTrRow);
+            float* tl = epi_tl;
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
@@ -435,18 +366,24 @@ void launch_head_mfma(const Head& h, int batch, const EpiArgs& ep, hipStream_t s
     const dim3 grid(ncb * ((ntg + 7u) / 8u) * 8u);
     const bool full = (B % ncol) == 0u;
     const bool pf2 = (h.G % 2u) == 0u;
-#define TDT_LAUNCH(NB, PF, OCC, FULL)                                                              \
-    hipExtLaunchKernelGGL((k_head_mfma<NB, PF, OCC, FULL>), grid, dim3(256), 0, st, ev0, ev1, 0, h.Wt, \
-                          h.SBt, h.x16, B, h.D, h.NC, h.G, ncb, ntg, ep)
-#define TDT_PICK(NB, OCC)                                                    \
-    do {                                                                     \
-        if (pf2) { if (full) TDT_LAUNCH(NB, 2, OCC, true); else TDT_LAUNCH(NB, 2, OCC, false); } \
-        else { if (full) TDT_LAUNCH(NB, 1, OCC, true); else TDT_LAUNCH(NB, 1, OCC, false); }     \
+#define TDT_LAUNCH(NB, PF, OCC, FULL, DN)                                                           \
+    hipExtLaunchKernelGGL((k_head_mfma<NB, PF, OCC, FULL, DN>), grid, dim3(256), 0, st, ev0, ev1, 0, h.Wt, \
+                          h.SB16t, h.x16, B, h.D, h.NC, h.G, ncb, ntg, ep)
+#define TDT_PICK2(NB, OCC, DN)                                                                     \
+    do {                                                                                           \
+        if (pf2) { if (full) TDT_LAUNCH(NB, 2, OCC, true, DN); else TDT_LAUNCH(NB, 2, OCC, false, DN); } \
+        else { if (full) TDT_LAUNCH(NB, 1, OCC, true, DN); else TDT_LAUNCH(NB, 1, OCC, false, DN); }     \
+    } while (0)
+#define TDT_PICK(NB, OCC)                                   \
+    do {                                                    \
+        if (h.mfma_denorm) TDT_PICK2(NB, OCC, true);        \
+        else TDT_PICK2(NB, OCC, false);                     \
     } while (0)
     if (nb == 1) TDT_PICK(1, 4);
     else if (nb == 2) TDT_PICK(2, 3);
     else TDT_PICK(4, 2);
 #undef TDT_PICK
+#undef TDT_PICK2
 #undef TDT_LAUNCH
     check_hip(hipGetLastError(), "head (MFMA)");
 }

@@ -539,7 +539,7 @@ __global__ __launch_bounds__(kMaxSplit * 64) void k_head_digits_split(
 // Workgroup size of the split kernel for this head: 64 * KS threads, or 0 when the head takes
 // one wave per tile instead. Enough waves to fill the chip (~2048) from few tiles.
 uint32_t split_threads(const Head& h) {
-    const uint32_t ks = std::min<uint32_t>({kMaxSplit, h.G, (2048u + h.ntile - 1u) / h.ntile});
+    const uint32_t ks = split_waves(h.G, h.ntile);
     return ks >= 2u ? 64u * ks : 0u;
 }
 
@@ -584,6 +584,106 @@ void launch_head_digits(const Head& h, int batch, const EpiArgs& ep, hipStream_t
     else
         throw std::runtime_error("digit GEMV supports batch 1 or 2");
     check_hip(hipGetLastError(), "head (digit GEMV)");
+}
+
+// ---- grouped matrix-vector products ---------------------------------------------------------
+// Several independent matrices, each with its own input row and output, in one launch: the
+// projections a token makes in one layer (the routed experts' gate and up matrices, or their down
+// matrices), each of which alone is a few microseconds of launch and round-trip latency at 1 - 6 MB.
+// Workgroup i serves tile i - tile_begin[m] of the matrix m whose range holds i; within it the work
+// is the folded split kernel's (digit planes of that matrix's row computed into LDS, KS waves
+// splitting the groups with the same split as one matrix alone, partial sums added in wave order),
+// so each output is bit-identical to the matrix's own call. The output is the raw product (no
+// softcap, no partials).
+__global__ __launch_bounds__(kMaxSplit * 64) void k_matvec_grouped(GroupArgs a) {
+    __shared__ float part[kMaxSplit][64];
+    __shared__ __attribute__((aligned(16))) FusedLds<1> fs;
+    const uint32_t lane = threadIdx.x & 63u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    uint32_t mi = 0;
+    for (uint32_t i = 1; i < a.count; ++i)
+        if (blockIdx.x >= a.m[i].tile_begin) mi = i;
+    const GroupMat M = a.m[mi];
+    const uint32_t tile = blockIdx.x - M.tile_begin;
+    const uint32_t D = M.D, G = D / kGroup, NC = D / 32u, KS = M.ks;
+    const bool active = wave < KS;
+    const uint32_t wv = active ? wave : 0u;  // idle waves load wave 0's range and drop it
+    const uint4* wp = M.Wt + (size_t)tile * NC * kTileRows + lane;
+    const uint32_t* sbp = M.SBt + (size_t)tile * G * kTileRows + lane;
+    const uint32_t g0 = wv * G / KS, g1 = (wv + 1u) * G / KS;
+    FusedPrep fp{};
+    fp.hidden = M.x;
+    fp.dtype = 0;
+    fp.normed = 1;
+    constexpr uint32_t kBatchG = 4;
+    uint4 Ab[kBatchG], Bb[kBatchG];
+    uint32_t Sb[kBatchG];
+    auto load_batch = [&](uint32_t gb) {
+#pragma unroll
+        for (uint32_t q = 0; q < kBatchG; ++q) {
+            const uint32_t g = min(gb + q, g1 - 1u);
+            Ab[q] = load_stream(wp + (size_t)(2 * g) * kTileRows);
+            Bb[q] = load_stream(wp + (size_t)(2 * g + 1) * kTileRows);
+            Sb[q] = load_stream(sbp + (size_t)g * kTileRows);
+        }
+    };
+    FusedIn<1> in;
+    fused_load<1>(fp, D, in);
+    __builtin_amdgcn_sched_barrier(0);
+    load_batch(g0);
+    __builtin_amdgcn_sched_barrier(0);
+    fused_prep<1>(fp, D, M.rows, in, fs);
+    float acc = 0.0f;
+    for (uint32_t gb = g0; gb < g1; gb += kBatchG) {
+        if (gb != g0) load_batch(gb);
+#pragma unroll
+        for (uint32_t q = 0; q < kBatchG; ++q) {
+            const bool inr = gb + q < g1;
+            const uint32_t g = min(gb + q, g1 - 1u);
+            const uint4 A = Ab[q], Bw = Bb[q];
+            const uint32_t sbw = Sb[q];
+            const uint32_t wq[8] = {A.x ^ 0x88888888u, A.y ^ 0x88888888u, A.z ^ 0x88888888u,
+                                    A.w ^ 0x88888888u, Bw.x ^ 0x88888888u, Bw.y ^ 0x88888888u,
+                                    Bw.z ^ 0x88888888u, Bw.w ^ 0x88888888u};
+            const float sf = bf16_to_f32(sbw & 0xFFFFu);
+            const float bf = bf16_to_f32(sbw >> 16);
+            const float c8 = fmaf(8.0f, sf, bf);
+            const uint32_t* xd = &fs.dig[0][(2u * g) * kDigitWordsPerChunk];
+            int d[kDigits];
+#pragma unroll
+            for (uint32_t k = 0; k < kDigits; ++k) d[k] = 0;
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (uint32_t k = 0; k < kDigits; ++k)
+                        d[k] = __builtin_amdgcn_sdot8((int)wq[4 * hh + i], (int)xd[hh * kDigitWordsPerChunk + k * 4 + i], d[k],
+                                                      false);
+            uint32_t Dg = (uint32_t)d[0];
+#pragma unroll
+            for (uint32_t k = 1; k < kDigits; ++k) Dg += (uint32_t)d[k] << (4u * k);
+            float t = fmaf((float)(int)Dg, sf * fs.ws[0][g], acc);
+            t = fmaf(c8, fs.sum[0][g], t);
+            acc = inr ? t : acc;
+        }
+    }
+    part[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0u) return;
+    float v = part[0][lane];
+    for (uint32_t w = 1; w < KS; ++w) v += part[w][lane];
+    const uint32_t row = tile * kTileRows + lane;
+    if (row < M.rows) M.out[row] = v;
+}
+
+void launch_matvec_grouped(const GroupArgs& a, uint32_t total_tiles, hipStream_t st) {
+    if (a.count == 0u) return;
+    hipLaunchKernelGGL(k_matvec_grouped, dim3(total_tiles), dim3(kMaxSplit * 64), 0, st, a);
+    check_hip(hipGetLastError(), "grouped int4 matvec");
+}
+
+uint32_t split_waves(uint32_t G, uint32_t ntile) {
+    return std::min<uint32_t>({kMaxSplit, G, (2048u + ntile - 1u) / ntile});
 }
 
 // Modifier epilogue over caller-provided logits (no softcap, no GEMV): one wave per 64 ids.

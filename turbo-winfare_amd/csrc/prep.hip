@@ -48,17 +48,67 @@ __global__ void k_repack_sb(const uint16_t* __restrict__ S, const uint16_t* __re
     SBt[it] = v;
 }
 
-void launch_repack(const Head& h, const uint8_t* W, const uint16_t* S, const uint16_t* B,
+// SB16t[tile][g][r] = fp16(S[row][g]) * 2^mul_log2 | fp16(B[row][g]) << 16 (zero past V). The
+// bf16 -> fp16 conversions round to nearest; the power-of-two scaling is exact unless it leaves
+// the fp16 range, which sets *bad.
+__global__ void k_repack_sb16(const uint16_t* __restrict__ S, const uint16_t* __restrict__ B,
+                              uint32_t* __restrict__ SB16t, uint32_t V, uint32_t G, uint64_t items, float mul,
+                              uint32_t* bad) {
+    const uint64_t it = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (it >= items) return;
+    const uint32_t r = (uint32_t)(it % kTileRows);
+    const uint64_t tg = it / kTileRows;
+    const uint32_t g = (uint32_t)(tg % G);
+    const uint64_t row = (tg / G) * kTileRows + r;
+    uint32_t v = 0u;
+    if (row < V) {
+        const _Float16 hs = (_Float16)bf16_to_f32(S[row * G + g]);
+        const _Float16 hm = (_Float16)((float)hs * mul);
+        const _Float16 hb = (_Float16)bf16_to_f32(B[row * G + g]);
+        if (!__builtin_isfinite((float)hm)) atomicOr(bad, 1u);
+        v = (uint32_t)__builtin_bit_cast(uint16_t, hm) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+    }
+    SB16t[it] = v;
+}
+
+void launch_repack_table(uint4* Wt, uint32_t* SBt, uint32_t V, uint32_t NC, uint32_t G, uint32_t ntile,
+                         const uint8_t* W, const uint16_t* S, const uint16_t* B, hipStream_t st) {
+    const uint64_t items_w = (uint64_t)ntile * NC * kTileRows;
+    const uint64_t items_sb = (uint64_t)ntile * G * kTileRows;
+    const uint32_t tpb = 256;
+    hipLaunchKernelGGL(k_repack_w, dim3((unsigned)((items_w + tpb - 1) / tpb)), dim3(tpb), 0, st, W, Wt, V, NC,
+                       items_w);
+    check_hip(hipGetLastError(), "repack weights");
+    hipLaunchKernelGGL(k_repack_sb, dim3((unsigned)((items_sb + tpb - 1) / tpb)), dim3(tpb), 0, st, S, B, SBt, V, G,
+                       items_sb);
+    check_hip(hipGetLastError(), "repack scales");
+}
+
+bool launch_repack(const Head& h, const uint8_t* W, const uint16_t* S, const uint16_t* B,
                    hipStream_t st) {
-    const uint64_t items_w = (uint64_t)h.ntile * h.NC * kTileRows;
+    launch_repack_table(h.Wt, h.SBt, h.V, h.NC, h.G, h.ntile, W, S, B, st);
     const uint64_t items_sb = (uint64_t)h.ntile * h.G * kTileRows;
     const uint32_t tpb = 256;
-    hipLaunchKernelGGL(k_repack_w, dim3((unsigned)((items_w + tpb - 1) / tpb)), dim3(tpb), 0, st,
-                       W, h.Wt, h.V, h.NC, items_w);
-    check_hip(hipGetLastError(), "repack weights");
-    hipLaunchKernelGGL(k_repack_sb, dim3((unsigned)((items_sb + tpb - 1) / tpb)), dim3(tpb), 0,
-                       st, S, B, h.SBt, h.V, h.G, items_sb);
-    check_hip(hipGetLastError(), "repack scales");
+    // the denormal dequant's s * 2^20 where every scale allows it, else plain s
+    uint32_t* bad = nullptr;
+    check_hip(hipMalloc(&bad, sizeof(uint32_t)), "alloc repack flag");
+    auto fill = [&](float mul, uint32_t* flag) -> hipError_t {
+        hipError_t e = hipMemsetAsync(bad, 0, sizeof(uint32_t), st);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(k_repack_sb16, dim3((unsigned)((items_sb + tpb - 1) / tpb)), dim3(tpb), 0, st, S, B,
+                           h.SB16t, h.V, h.G, items_sb, mul, bad);
+        e = hipGetLastError();
+        if (e == hipSuccess) e = hipMemcpyAsync(flag, bad, sizeof(uint32_t), hipMemcpyDeviceToHost, st);
+        if (e == hipSuccess) e = hipStreamSynchronize(st);
+        return e;
+    };
+    uint32_t flag = 0u;
+    hipError_t e = fill(1048576.0f, &flag);
+    const bool denorm = e == hipSuccess && flag == 0u;
+    if (e == hipSuccess && !denorm) e = fill(1.0f, &flag);
+    (void)hipFree(bad);
+    check_hip(e, "repack fp16 scales");
+    return denorm;
 }
 
 // ---- per-step preparation (one launch) -------------------------------------------------------
@@ -78,8 +128,9 @@ void launch_repack(const Head& h, const uint8_t* W, const uint16_t* S, const uin
 // one packed word per digit.
 //
 // fp16 (MFMA path): x rounded to fp16 and stored k-permuted within each octet as
-// (x0, x4, x1/16, x5/16, x2, x6, x3/16, x7/16): the order in which the weight dequant produces
-// halves, with odd elements divided by 16 because their weight halves carry a factor 16.
+// (x0, x4, x1, x5, x2, x6, x3, x7), the order in which the weight dequant produces halves, with
+// the even elements times 16 (denormal dequant, whose even weight halves carry 1/16) or the odd
+// elements divided by 16 (the other dequant, whose odd weight halves carry 16).
 //
 // History counts: the occurrences of each id < V (merged per id in LDS first) are added to
 // hcount[b][id] and the id's bit is set in hbits[b] (global atomics); the head epilogue zeroes
@@ -169,7 +220,7 @@ __device__ void prep_row(const PrepArgs& a, uint32_t b, uint32_t k) {
     } else {
         const uint32_t e = i & 7u;
         const uint32_t slot = (e < 4u) ? 2u * e : 2u * (e - 4u) + 1u;
-        const _Float16 hv = (_Float16)((e & 1u) ? v * 0.0625f : v);
+        const _Float16 hv = (_Float16)(a.x16_denorm ? ((e & 1u) ? v : v * 16.0f) : ((e & 1u) ? v * 0.0625f : v));
         a.x16[(size_t)b * D + (i & ~7u) + slot] = __builtin_bit_cast(uint16_t, hv);
     }
 }

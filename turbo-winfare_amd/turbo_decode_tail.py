@@ -52,6 +52,10 @@ EXPORTS = (
     "turbo_bundle_find_tensor",
     "turbo_lmhead_create_from_bundle",
     "turbo_sample_logits_noalloc",
+    "turbo_int4_matrix_create",
+    "turbo_int4_matrix_load",
+    "turbo_int4_matrix_destroy",
+    "turbo_int4_matvec_grouped",
 )
 
 TURBO_NOALLOC_MAX_BATCH = 4
@@ -195,6 +199,10 @@ def load(path: os.PathLike | str | None = None) -> C.CDLL:
         "turbo_lmhead_create_from_bundle": (vp, [C.c_char_p, f32, f32, i32]),
         "turbo_sample_logits_noalloc": (i32, [vp, u32, f32, vp, C.POINTER(TurboStepInputs),
                                               C.POINTER(TurboStepOutputs)]),
+        "turbo_int4_matrix_create": (vp, [u32, u32, i32]),
+        "turbo_int4_matrix_load": (i32, [vp, vp, vp, vp, i32, vp]),
+        "turbo_int4_matrix_destroy": (None, [vp]),
+        "turbo_int4_matvec_grouped": (i32, [C.POINTER(vp), i32, C.POINTER(vp), C.POINTER(vp), vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -375,6 +383,42 @@ class LMHead:
         ms, n = C.c_double(), C.c_int()
         _ok(self.lib.turbo_lmhead_head_kernel_time(self.h, C.byref(ms), C.byref(n), 1 if reset else 0))
         return ms.value, n.value
+
+
+class Int4Matrix:
+    """One turbo_int4_matrix handle (the table only). Arrays: numpy (host) or torch CUDA tensors."""
+
+    def __init__(self, rows: int, in_dim: int, device: int = 0):
+        self.lib = load()
+        self.rows, self.in_dim = rows, in_dim
+        self.h = self.lib.turbo_int4_matrix_create(rows, in_dim, device)
+        if not self.h:
+            raise TurboError(last_error())
+
+    def load_weights(self, weight, scales, biases, *, on_device: bool = False, stream=None) -> None:
+        hp = (lambda a: _ptr(a)) if on_device else (lambda a: a.ctypes.data)
+        _ok(self.lib.turbo_int4_matrix_load(self.h, hp(weight), hp(scales), hp(biases), 1 if on_device else 0,
+                                            stream))
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            self.lib.turbo_int4_matrix_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def matvec_grouped(matrices, xs, outs, stream=None) -> None:
+    """turbo_int4_matvec_grouped: out[i] = matrices[i] @ xs[i], one launch (device buffers)."""
+    n = len(matrices)
+    mats = (C.c_void_p * max(n, 1))(*[m.h for m in matrices])
+    xp = (C.c_void_p * max(n, 1))(*[_ptr(x) for x in xs])
+    op = (C.c_void_p * max(n, 1))(*[_ptr(o) for o in outs])
+    _ok(load().turbo_int4_matvec_grouped(mats, n, xp, op, stream))
 
 
 def sample_logits_noalloc(logits, vocab: int, inp: TurboStepInputs, tokens, report=None, *,
