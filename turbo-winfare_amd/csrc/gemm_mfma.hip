@@ -230,26 +230,42 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
                 s = bs[0];
                 e = bs[1];
             }
-            if ((hb[0] | hb[1]) != 0u || s < e) {
+            // bias first (the order of apply_entry): entries are unique per id, so each is read
+            // once and added to the one register that holds its id, if this lane holds it
+            for (uint32_t k = s; k < e; ++k) {
+                const ModEntry t = me[k];
+                const uint32_t rr = t.id - base;
 #pragma unroll
                 for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        if (rr == 32u * mb + acc_row(r, hl)) {
+#pragma clang fp contract(off)
+                            acc[mb][nb][r] = acc[mb][nb][r] + t.bias;
+                        }
+            }
+            // history counts: all loads of a 32-row half are issued before any is consumed, then
+            // each read count is zeroed for the next step and applied
+            if ((hb[0] | hb[1]) != 0u) {
+                uint32_t* hrow = ep.hcount + (size_t)bq * ep.V + base;
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb) {
+                    if (hb[mb] == 0u) continue;
+                    uint32_t cnt[16];
+#pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const uint32_t rr = 32u * mb + acc_row(r, hl);
-                        const uint32_t id = base + rr;
-                        ModEntry m{id, 0u, 0.0f, 0u};
-                        if ((hb[mb] >> (rr & 31u)) & 1u) {
-                            uint32_t* cp = ep.hcount + (size_t)bq * ep.V + id;
-                            m.count = *cp;
-                            if (m.count) *cp = 0u;  // read once per step; zeroed for the next
-                        }
-                        for (uint32_t k = s; k < e; ++k) {
-                            const ModEntry t = me[k];
-                            if (t.id == id) { m.bias = t.bias; m.has_bias = 1u; }
-                        }
-                        if (m.count || m.has_bias)
-                            acc[mb][nb][r] = apply_entry(acc[mb][nb][r], m, row, ep.rep_limit);
+                        cnt[r] = ((hb[mb] >> (rr & 31u)) & 1u) ? hrow[rr] : 0u;
                     }
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        if (cnt[r]) {
+                            const uint32_t rr = 32u * mb + acc_row(r, hl);
+                            hrow[rr] = 0u;
+                            acc[mb][nb][r] = apply_entry(acc[mb][nb][r], ModEntry{base + rr, cnt[r], 0.0f, 0u}, row,
+                                                         ep.rep_limit);
+                        }
+                }
             }
         }
         if (col_ok && ep.ban) {
