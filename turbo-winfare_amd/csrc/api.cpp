@@ -402,8 +402,10 @@ int run_rows(Head& h, HandleBox* bx, const TurboStepInputs* in, const TurboStepO
         for (int b = 0; b < B; ++b) fp.inl[b] = rows[b];
         tdt::EpiArgs ep = epi_args(h, logits, true);
         ep.no_sumexp = any_short ? 0u : 1u;
+        ep.no_smax = any_short ? 0u : 1u;
         ep.ban = in->ban_bits;
         ep.ban_stride = in->ban_stride;
+        ep.meta = (any_mods || in->ban_bits) ? 1u : 0u;
         launch_head(*bx, B, ep, &fp);
     }
 
@@ -431,8 +433,10 @@ int run_rows(Head& h, HandleBox* bx, const TurboStepInputs* in, const TurboStepO
         release_slot(h, pos);
         tdt::EpiArgs ep = epi_args(h, logits, hidden != nullptr);
         ep.no_sumexp = any_short ? 0u : 1u;  // greedy and full-vocabulary rows do not read them
+        ep.no_smax = any_short ? 0u : 1u;
         ep.ban = in->ban_bits;
         ep.ban_stride = in->ban_stride;
+        ep.meta = (any_mods || in->ban_bits) ? 1u : 0u;
         if (hidden) launch_head(*bx, B, ep);
         else tdt::launch_logits_epilogue(h, B, ep, h.stream);
     }

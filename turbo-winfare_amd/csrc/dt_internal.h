@@ -109,6 +109,10 @@ struct EpiArgs {
     float rep_limit;           // 0.9999 * softcap used by the repetition clamp (0 = none)
     uint32_t no_sumexp;        // 1: no row samples from a shortlist, so the block sums of
                                // exp(l - max) are not needed and stay 0
+    uint32_t no_smax;          // 1: no row samples from a shortlist, so the blocks' second
+                               // largest values are not needed (left -inf by the MFMA head)
+    uint32_t meta;             // 1: some row has modifiers or a ban mask (the MFMA head stages
+                               // their words in LDS); 0: the MFMA head skips modifiers and ban
 };
 
 enum class HeadPath { Digits, Mfma };

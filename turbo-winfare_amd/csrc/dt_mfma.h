@@ -96,12 +96,86 @@ __device__ inline float softcap_fast(float z, float cap, float inv_cap) {
     return cap * copysignf(t, x);
 }
 
+// Softcap cap * tanh(z / cap) as z * P(u), u = z^2, for |z| <= cap / 2: P is a degree-5
+// polynomial fitted to tanh(x) / x over x^2 in [0, 1/4] (coefficients c_i of x^(2i), Chebyshev-node
+// least squares), pre-scaled by cap^(-2i). In fp32 with fused multiply-adds it stays within
+// 1e-7 relative of the exact softcap, closer than fp32 cap * tanhf(z / cap) itself (which rounds
+// z / cap first). A wave with any larger |z| takes softcap_fast for all its values.
+struct SoftcapPoly {
+    float k1, k2, k3, k4, k5;  // c_i / cap^(2i)
+    float lim;                 // cap / 2
+    float inv;                 // 1 / cap
+};
+__device__ inline SoftcapPoly softcap_poly(float cap) {
+    SoftcapPoly p;
+    p.inv = 1.0f / cap;
+    const float i2 = p.inv * p.inv, i4 = i2 * i2;
+    p.k1 = -0.33333325f * i2;
+    p.k2 = 0.13332954f * i4;
+    p.k3 = -0.053898074f * (i4 * i2);
+    p.k4 = 0.021292942f * (i4 * i4);
+    p.k5 = -0.0066395057f * (i4 * i4 * i2);
+    p.lim = 0.5f * cap;
+    return p;
+}
+template <int N>
+__device__ inline void softcap_values(float (&z)[N], const SoftcapPoly& p, float cap) {
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < N; ++i) m = fmaxf(m, fabsf(z[i]));
+    if (__builtin_amdgcn_ballot_w64(m > p.lim) != 0ull) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) z[i] = softcap_fast(z[i], cap, p.inv);
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const float u = z[i] * z[i];
+        float q = fmaf(p.k5, u, p.k4);
+        q = fmaf(q, u, p.k3);
+        q = fmaf(q, u, p.k2);
+        q = fmaf(q, u, p.k1);
+        q = fmaf(q, u, 1.0f);
+        z[i] = z[i] * q;
+    }
+}
+
+// Modifier words of a workgroup's (tile, column) pairs, staged in LDS before the main loop:
+// w[t][c] = {history bitmap word 0, word 1, ban word 0, word 1, first bias entry, end}; and per
+// column r[c] = {has_mods, repetition, presence, frequency penalty bits}.
+template <uint32_t NCOL>
+struct EpiMeta {
+    uint32_t w[4][NCOL][6];
+    uint32_t r[NCOL][4];
+};
+
+// Word 3 of a raw buffer resource on this architecture (32-bit data format, no swizzle).
+constexpr int kBufDword3 = 0x00020000;
+// Cache policy of the streamed loads: nontemporal.
+constexpr int kNt = 2;
+// s_waitcnt operand that waits until at most n vector-memory operations are outstanding and
+// leaves the other counters unconstrained (vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+constexpr int vm_wait(uint32_t n) { return (int)((n & 15u) | (7u << 4) | (15u << 8) | ((n >> 4) << 14)); }
+
+// Buffer loads (nontemporal) at a per-lane byte offset plus a wave-uniform one, and the
+// buffer-to-LDS form: 16 bytes per lane to lds + 16 * lane, counted by vmcnt like any load.
+__device__ inline uint4 buf_load_b128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    const v4u t = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kNt);
+    return make_uint4(t.x, t.y, t.z, t.w);
+}
+__device__ inline uint32_t buf_load_b32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, kNt);
+}
+__device__ inline void buf_dma_16(__amdgpu_buffer_rsrc_t r, unsigned char* lds, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+}
+
+// Floats of one wave's transposed half tile (32 columns x 32 rows) in the epilogue.
+constexpr uint32_t kTrHalfFloats = 32u * 32u;
+
 // Row held in register r of a 32x32 accumulator by a lane with half hl (0/1): 8(r/4) + 4hl + r%4.
 __device__ inline uint32_t acc_row(int r, uint32_t hl) { return 8u * (uint32_t)(r >> 2) + 4u * hl + (uint32_t)(r & 3); }
 
 __device__ inline uint32_t word_of(const uint4& w, int j) { return (j == 0) ? w.x : (j == 1) ? w.y : (j == 2) ? w.z : w.w; }
-
-// Row pitch (floats) of a wave's LDS transpose tile in the head's epilogue.
-constexpr uint32_t kTrRow = 68;
 
 }  // namespace tdt

@@ -24,6 +24,7 @@
 #include <hip/hip_ext.h>
 
 #include <stdexcept>
+#include <type_traits>
 #include <utility>
 
 #include "dt_mfma.h"
@@ -38,16 +39,29 @@ namespace tdt {
 // last group are clamped to it and never used, so the compiler's load counters stay exact and
 // the weight prefetch is never drained early. The next k-step's weights are dequantised in
 // the shadow of the current step's MFMAs.
-template <int NB, int PF, int OCC, bool FULL, bool DENORM>
+// META: some row has modifiers or a ban mask; the workgroup's per-(tile, column) modifier words
+// are then staged in LDS before the main loop (their loads issue ahead of the weight stream), so
+// the epilogue reads them from LDS instead of waiting on global loads.
+template <int NB, int PF, int OCC, bool DENORM, bool META>
 __global__ __launch_bounds__(256, OCC) void k_head_mfma(
     const uint4* __restrict__ Wt, const uint32_t* __restrict__ SB16t,
     const uint16_t* __restrict__ x16, uint32_t B, uint32_t D, uint32_t NC, uint32_t G, uint32_t ncb, uint32_t ntg, EpiArgs ep) {
     constexpr uint32_t NT = 256;
     constexpr uint32_t NCOL = 32 * NB;
-    constexpr uint32_t XP = NCOL * 8;                 // 16-byte activation pieces per group
-    constexpr uint32_t XPT = XP / NT;
-    static_assert(XP % NT == 0, "activation pieces must split evenly over the threads");
-    __shared__ __attribute__((aligned(16))) _Float16 lx[2][NCOL * kColHalves];
+    // Activations: group g (NCOL columns x 64 halves) lives in stage g % NST of a ring in LDS,
+    // written by buffer-to-LDS DMA PF - 1 groups ahead (no registers, no LDS store instructions).
+    // Column c holds its eight 16-byte pieces p at slot c * 8 + (p ^ ((c >> 1) & 7)): the MFMA's
+    // fragment reads (16 lanes = 16 consecutive columns, one piece) then hit 64 distinct banks.
+    constexpr uint32_t kStage = NCOL * 128u;
+    constexpr uint32_t NST = PF > 1 ? PF : 2;
+    constexpr uint32_t XDMA = kStage / (NT * 16u);  // DMA instructions per thread per group
+    static_assert(kStage % (NT * 16u) == 0u, "a stage must split into whole 1 KiB DMA rows per wave");
+    constexpr uint32_t kXBytes = NST * kStage;
+    constexpr uint32_t kTrBytes = 4u * kTrHalfFloats * 4u;  // the epilogue's four transposed half tiles
+    constexpr uint32_t kPoolBytes = kXBytes > kTrBytes ? kXBytes : kTrBytes;
+    constexpr uint32_t kLdsBytes = kPoolBytes + (META ? (uint32_t)sizeof(EpiMeta<NCOL>) : 0u);
+    __shared__ __attribute__((aligned(16))) unsigned char pool[kLdsBytes];
+    EpiMeta<NCOL>& meta = *reinterpret_cast<EpiMeta<NCOL>*>(pool + kPoolBytes);  // used only when META
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     // Workgroup i is dispatched to XCD i % 8. The ncb column blocks of one group of four tiles go
@@ -62,33 +76,39 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
     const uint32_t tile = tile_ok ? tile_raw : ep.ntile - 1u;  // clamp loads; skip the epilogue
     const uint32_t hl = lane >> 5, l32 = lane & 31u;
 
-    const uint4* wbase = Wt + (size_t)tile * NC * kTileRows + (size_t)hl * kTileRows + l32;
-    const uint32_t* sbbase = SB16t + (size_t)tile * G * kTileRows + l32;
-    auto wload = [&](uint32_t g, int mb) { return mfma_load_stream(wbase + (size_t)(2u * g) * kTileRows + 32u * mb); };
-    auto sload = [&](uint32_t g, int mb) { return mfma_load_stream(sbbase + (size_t)g * kTileRows + 32u * mb); };
+    // Weights and scales through buffer loads: a per-lane byte offset plus the group's offset in
+    // an SGPR, so no address arithmetic runs per load.
+    const __amdgpu_buffer_rsrc_t wrs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint4*>(Wt), 0, ep.ntile * NC * kTileRows * 16u, kBufDword3);
+    const __amdgpu_buffer_rsrc_t srs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(SB16t), 0, ep.ntile * G * kTileRows * 4u, kBufDword3);
+    const uint32_t woff = ((tile * NC + hl) * kTileRows + l32) * 16u;
+    const uint32_t soff = (tile * G * kTileRows + l32) * 4u;
+    auto wload = [&](uint32_t g, int mb) { return buf_load_b128(wrs, woff + 512u * (uint32_t)mb, g * 2048u); };
+    auto sload = [&](uint32_t g, int mb) { return buf_load_b32(srs, soff + 128u * (uint32_t)mb, g * 256u); };
     const uint32_t magic = DENORM ? 0u : magic_vgpr();
 
-    auto load_x = [&](uint32_t g, v4u* xr) {
+    // The DMA sources of this thread's pieces: instruction i of wave w fills slots
+    // (4 i + w) * 64 + lane of a stage. Columns past the batch read past the buffer's end (zeros).
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x16), 0, B * D * 2u, kBufDword3);
+    uint32_t xoff[XDMA];
 #pragma unroll
-        for (uint32_t p = 0; p < XPT; ++p) {
-            const uint32_t pc = tid + p * NT;
-            const uint32_t n = cbase + (pc >> 3), o = pc & 7u;
-            if constexpr (FULL) {
-                xr[p] = *reinterpret_cast<const v4u*>(x16 + (size_t)n * D + 64u * g + 8u * o);
-            } else {
-                v4u v = {0u, 0u, 0u, 0u};
-                if (n < B) v = *reinterpret_cast<const v4u*>(x16 + (size_t)n * D + 64u * g + 8u * o);
-                xr[p] = v;
-            }
-        }
-    };
-    auto store_x = [&](uint32_t buf, const v4u* xr) {
+    for (uint32_t i = 0; i < XDMA; ++i) {
+        const uint32_t sl = (4u * i + wave) * 64u + lane, c = sl >> 3, pc = (sl & 7u) ^ ((c >> 1) & 7u);
+        xoff[i] = (cbase + c < B) ? ((cbase + c) * D + 8u * pc) * 2u : B * D * 2u;
+    }
+    auto dma_x = [&](uint32_t g, uint32_t st) {
 #pragma unroll
-        for (uint32_t p = 0; p < XPT; ++p) {
-            const uint32_t pc = tid + p * NT;
-            *reinterpret_cast<v4u*>(&lx[buf][(pc >> 3) * kColHalves + 8u * (pc & 7u)]) = xr[p];
-        }
+        for (uint32_t i = 0; i < XDMA; ++i) buf_dma_16(xrs, pool + st * kStage + (4u * i + wave) * 1024u, xoff[i], g * 128u);
     };
+    // Every iteration issues, in this order, the DMA of a later group's activations, two scale
+    // loads and two weight loads. The DMA of group g + 1 is issued in iteration g + 2 - PF: when
+    // iteration g ends, its own iteration's four loads and PF - 2 whole iterations followed it, so
+    // waiting until at most that many are outstanding waits for it (with PF = 1 it was issued in
+    // iteration g itself). Where the DMA came from the prologue more followed it: the wait is
+    // stricter than needed there.
+    constexpr uint32_t kXWait = (PF > 1) ? 4u + (PF - 2u) * (XDMA + 4u) : 4u;
+    static_assert(kXWait < 64u, "vmcnt holds 6 bits");
 
     f16v acc[2][NB];
 #pragma unroll
@@ -98,21 +118,87 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[mb][nb][r] = 0.0f;
 
-    // Weights and activations are prefetched PF groups ahead in the same slots, in the same
-    // order: the load counter is in-order, so waiting for a group's activations (at the LDS
-    // store) only waits for loads that the next group needs anyway.
+    // The modifier words of the workgroup's (tile, column) pairs, loaded before the weight
+    // stream; they are stored to LDS after the prologue's wait, which covers them.
+    constexpr uint32_t kMetaPer = (4u * NCOL + NT - 1u) / NT;
+    uint32_t mw[META ? kMetaPer : 1][6];
+    uint32_t mr[META ? kMetaPer : 1][4];
+    if constexpr (META) {
+#pragma unroll
+        for (uint32_t q = 0; q < kMetaPer; ++q) {
+            const uint32_t idx = tid + q * NT, t = idx / NCOL, c = cbase + idx % NCOL, tl = tg * 4u + t;
+#pragma unroll
+            for (int k = 0; k < 6; ++k) mw[q][k] = 0u;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) mr[q][k] = 0u;
+            if (idx < 4u * NCOL && c < B && tl < ep.ntile) {
+                const uint32_t* rw = reinterpret_cast<const uint32_t*>(ep.rows + c);
+                mr[q][0] = rw[9];  // has_mods
+                mr[q][1] = rw[3];  // repetition_penalty
+                mr[q][2] = rw[4];  // presence_penalty
+                mr[q][3] = rw[5];  // frequency_penalty
+                const bool two = tl * kTileRows + 32u < ep.V;
+                if (ep.hcount) {
+                    const uint32_t* hw = ep.hbits + (size_t)c * ep.hbw + 2u * tl;
+                    mw[q][0] = hw[0];
+                    if (two) mw[q][1] = hw[1];
+                }
+                if (ep.ban) {
+                    const uint32_t* bw = ep.ban + (size_t)c * ep.ban_stride + 2u * tl;
+                    mw[q][2] = bw[0];
+                    if (two) mw[q][3] = bw[1];
+                }
+                if (ep.block_start) {
+                    const uint32_t* bs = ep.block_start + (size_t)c * (ep.ntile + 1u) + tl;
+                    mw[q][4] = bs[0];
+                    mw[q][5] = bs[1];
+                }
+            }
+        }
+    }
+
+    // Prologue: weights of groups 0 .. PF - 1, activations of groups 0 .. PF - 2 (PF = 1: group 0),
+    // each clamped to the last group.
     uint4 wr[PF][2];
     uint32_t sbr[PF][2];
-    v4u xr[PF][XPT];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int p = 0; p < PF; ++p) {
         const uint32_t gp = min((uint32_t)p, G - 1u);
+        if (p < PF - 1 || PF == 1) dma_x(gp, (uint32_t)p);
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb) { wr[p][mb] = wload(gp, mb); sbr[p][mb] = sload(gp, mb); }
-        load_x(gp, xr[p]);
+        for (int mb = 0; mb < 2; ++mb) sbr[p][mb] = sload(gp, mb);
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) wr[p][mb] = wload(gp, mb);
+        __builtin_amdgcn_sched_barrier(0);
     }
-    store_x(0, xr[0]);
-    __syncthreads();
+    if constexpr (META) {
+        __builtin_amdgcn_s_waitcnt(vm_wait(kXWait));  // the modifier loads came first
+#pragma unroll
+        for (uint32_t q = 0; q < kMetaPer; ++q) {
+            const uint32_t idx = tid + q * NT;
+            if (idx < 4u * NCOL) {
+                const uint32_t t = idx / NCOL, cl = idx % NCOL;
+#pragma unroll
+                for (int k = 0; k < 6; ++k) meta.w[t][cl][k] = mw[q][k];
+                if (t == 0u) {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) meta.r[cl][k] = mr[q][k];
+                }
+            }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(vm_wait(kXWait));  // this thread's pieces of group 0
+    __builtin_amdgcn_s_barrier();
+
+    // fragment offsets within a stage: column 32 nb + l32, piece 4 hl + j
+    const uint32_t sw = (l32 >> 1) & 7u;
+    uint32_t foff[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) foff[j] = l32 * 128u + (((4u * hl + (uint32_t)j) ^ sw) << 4);
+    auto bfrag = [&](uint32_t st, int j, int nb) {
+        return *reinterpret_cast<const h8v*>(pool + st * kStage + foff[j] + 4096u * (uint32_t)nb);
+    };
 
     h8v acur[2], anext[2];
 #pragma unroll
@@ -120,31 +206,31 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
         const SbHalves h = unpack_sb16<DENORM>(sbr[0][mb]);
         acur[mb] = dequant_word<DENORM>(wr[0][mb].x, h.s2, h.b2, h.bx, magic);
     }
-    uint32_t buf = 0;
     for (uint32_t g0 = 0; g0 < G; g0 += PF) {
 #pragma unroll
         for (int p = 0; p < PF; ++p) {
             const uint32_t g = g0 + p;
+            // stage of group g; group g + PF - 1 goes to the stage group g - 1 used (every wave
+            // finished with it before the last barrier)
+            const uint32_t st = (PF > 1) ? (uint32_t)p : (g & 1u);
+            const uint32_t stn = (PF > 1) ? (uint32_t)((p + PF - 1) % PF) : ((g + 1u) & 1u);
             uint4 wc[2];
             SbHalves hc[2];
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb) { wc[mb] = wr[p][mb]; hc[mb] = unpack_sb16<DENORM>(sbr[p][mb]); }
-            // slot p held group g, whose activations are already in LDS: refill it with g + PF
+            const uint32_t gx = min(g + (uint32_t)(PF > 1 ? PF - 1 : 1), G - 1u);
             const uint32_t gn = min(g + (uint32_t)PF, G - 1u);
+            __builtin_amdgcn_sched_barrier(0);
+            dma_x(gx, stn);
 #pragma unroll
-            for (int mb = 0; mb < 2; ++mb) { wr[p][mb] = wload(gn, mb); sbr[p][mb] = sload(gn, mb); }
-            load_x(gn, xr[p]);
+            for (int mb = 0; mb < 2; ++mb) sbr[p][mb] = sload(gn, mb);
+            __builtin_amdgcn_sched_barrier(0);
             constexpr int kNext = (PF > 1) ? 1 : 0;
             const int pn = (p + kNext) % PF;         // prefetch slot holding group g + 1
-            const _Float16* lb = &lx[buf][0];
             // with four column blocks the activation fragments are read one (j, nb) ahead of their
-            // MFMAs, so no MFMA pair waits for the LDS read just issued (measured 1.7 % faster
-            // there; not at one column block)
-            auto bfrag = [&](int j, int nb) {
-                return *reinterpret_cast<const h8v*>(lb + (32u * (uint32_t)nb + l32) * kColHalves + 32u * hl + 8u * (uint32_t)j);
-            };
-            constexpr bool kAhead = NB == 4 && FULL;  // (the partial-column variant would spill)
-            h8v bcur = bfrag(0, 0);
+            // MFMAs, so no MFMA pair waits for the LDS read just issued
+            constexpr bool kAhead = NB == 4;
+            h8v bcur = bfrag(st, 0, 0);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
 #pragma unroll
@@ -156,15 +242,23 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
                         anext[mb] = dequant_word<DENORM>(wr[pn][mb].x, h.s2, h.b2, h.bx, magic);
                     }
                 }
+                if (j == 2) {
+                    // the last use of this slot's weights is behind: refill it with group g + PF
+                    // (its registers are reused in place, with no copy at the loop's end)
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int mb = 0; mb < 2; ++mb) wr[p][mb] = wload(gn, mb);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb) {
                     h8v bv, bnext = bcur;
                     if constexpr (kAhead) {
                         bv = bcur;
-                        if (nb + 1 < NB) bnext = bfrag(j, nb + 1);
-                        else if (j < 3) bnext = bfrag(j + 1, 0);
+                        if (nb + 1 < NB) bnext = bfrag(st, j, nb + 1);
+                        else if (j < 3) bnext = bfrag(st, j + 1, 0);
                     } else {
-                        bv = bfrag(j, nb);
+                        bv = bfrag(st, j, nb);
                     }
 #pragma unroll
                     for (int mb = 0; mb < 2; ++mb)
@@ -181,190 +275,196 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
 #pragma unroll
                 for (int mb = 0; mb < 2; ++mb) acur[mb] = anext[mb];
             }
-            store_x(buf ^ 1u, xr[(p + 1) % PF]);  // group g + 1 (clamped), loaded PF - 1 groups ago
-            __syncthreads();
-            buf ^= 1u;
+            // group g + 1's activations: this thread's pieces, then everyone's
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(vm_wait(kXWait));
+            __builtin_amdgcn_s_barrier();
         }
     }
+    // The clamped DMAs past the last group may still be writing the ring; the epilogue reuses it.
+    __builtin_amdgcn_s_waitcnt(vm_wait(0u));
+    __builtin_amdgcn_s_barrier();
     if (!tile_ok) return;
 
     // ---- epilogue, in place on the accumulators ----
-    // The transposed logit stores (four column blocks) reuse the activation buffer: one
-    // 32 x kTrRow float tile per wave, after every wave's last read of it (the main loop ends
-    // with a barrier).
-    constexpr bool kTransposeStores = NB == 4;
-    static_assert(!kTransposeStores || sizeof(lx) >= 4u * 32u * kTrRow * sizeof(float),
-                  "four wave tiles must fit the activation buffer");
-    float* epi_tl = reinterpret_cast<float*>(&lx[0][0]) + wave * (32u * kTrRow);
+    // Lane (l32, hl) holds batch column cbase + 32 nb + l32 and, per 32-row half mb, the 16 rows
+    // 32 mb + acc_row(r, hl) of the wave's tile, in increasing order over (mb, r).
     const uint32_t base = tile * kTileRows;
-    const bool vec_ok = (ep.V & 3u) == 0u;  // float4 stores need 16-byte aligned rows
     const bool full_tile = base + kTileRows <= ep.V;
-    const float inv_cap = (ep.cap > 0.0f) ? 1.0f / ep.cap : 0.0f;
-    // One column block at a time, indexed at compile time so the accumulators stay in registers.
+    const bool vec_ok = (ep.V & 3u) == 0u;  // float4 stores need 16-byte aligned rows
+    float* tr = reinterpret_cast<float*>(pool) + wave * kTrHalfFloats;
+    SoftcapPoly sc;
+    if (ep.cap > 0.0f) sc = softcap_poly(ep.cap);
     auto column = [&]<int nb>() {
         const uint32_t bcol = cbase + 32u * nb + l32;
         const bool col_ok = bcol < B;
         const uint32_t bq = col_ok ? bcol : 0u;
-        if (ep.cap > 0.0f) {
-#pragma unroll
-            for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[mb][nb][r] = softcap_fast(acc[mb][nb][r], ep.cap, inv_cap);
-        }
-        if (col_ok && ep.rows[bq].has_mods) {
-            const DevRow row = ep.rows[bq];
-            // history counts: the two bitmap words of this tile decide which ids to look up
-            // (both halves of the column read them; the low half zeroes them for the next step)
-            uint32_t hb[2] = {0u, 0u};
-            if ((row.has_mods & 1u) && ep.hcount) {
-                uint32_t* hw = ep.hbits + (size_t)bq * ep.hbw + (base >> 5);
-                hb[0] = hw[0];
-                if (base + 32u < ep.V) hb[1] = hw[1];
-                if (hl == 0u && hb[0] != 0u) hw[0] = 0u;
-                if (hl == 0u && hb[1] != 0u) hw[1] = 0u;
-            }
-            uint32_t s = 0, e = 0;
-            const ModEntry* me = ep.mods + (size_t)bq * ep.mod_cap;
-            if ((row.has_mods & 2u) && ep.block_start) {
-                const uint32_t* bs = ep.block_start + (size_t)bq * (ep.ntile + 1) + tile;
-                s = bs[0];
-                e = bs[1];
-            }
-            // bias first (the order of apply_entry): entries are unique per id, so each is read
-            // once and added to the one register that holds its id, if this lane holds it
-            for (uint32_t k = s; k < e; ++k) {
-                const ModEntry t = me[k];
-                const uint32_t rr = t.id - base;
-#pragma unroll
-                for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        if (rr == 32u * mb + acc_row(r, hl)) {
-#pragma clang fp contract(off)
-                            acc[mb][nb][r] = acc[mb][nb][r] + t.bias;
-                        }
-            }
-            // history counts: all loads of a 32-row half are issued before any is consumed, then
-            // each read count is zeroed for the next step and applied
-            if ((hb[0] | hb[1]) != 0u) {
-                uint32_t* hrow = ep.hcount + (size_t)bq * ep.V + base;
-#pragma unroll
-                for (int mb = 0; mb < 2; ++mb) {
-                    if (hb[mb] == 0u) continue;
-                    uint32_t cnt[16];
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const uint32_t rr = 32u * mb + acc_row(r, hl);
-                        cnt[r] = ((hb[mb] >> (rr & 31u)) & 1u) ? hrow[rr] : 0u;
-                    }
-#pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        if (cnt[r]) {
-                            const uint32_t rr = 32u * mb + acc_row(r, hl);
-                            hrow[rr] = 0u;
-                            acc[mb][nb][r] = apply_entry(acc[mb][nb][r], ModEntry{base + rr, cnt[r], 0.0f, 0u}, row,
-                                                         ep.rep_limit);
-                        }
-                }
-            }
-        }
-        if (col_ok && ep.ban) {
-            const uint32_t* bw = ep.ban + (size_t)bq * ep.ban_stride + (base >> 5);
-            const uint32_t ban0 = bw[0];
-            const uint32_t ban1 = (base + 32u < ep.V) ? bw[1] : 0u;
-#pragma unroll
-            for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const uint32_t rr = 32u * mb + acc_row(r, hl);
-                    if ((((mb == 0) ? ban0 : ban1) >> (rr & 31u)) & 1u) acc[mb][nb][r] = -INFINITY;
-                }
-        }
-        if (!full_tile) {
-#pragma unroll
-            for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    if (base + 32u * mb + acc_row(r, hl) >= ep.V) acc[mb][nb][r] = -INFINITY;
-        }
-        float bmax = -INFINITY, bmin = INFINITY, bsec = -INFINITY;  // bsec: second largest, with repeats
-        uint32_t barg = 0xFFFFFFFFu;
+        // acc[mb][nb] for mb = 0, 1 as one array of 32 values in row order
+        float zz[32];
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float z = acc[mb][nb][r];
-                if (z > bmax) {  // rows in increasing order
-                    bsec = bmax;
-                    bmax = z;
-                    barg = base + 32u * mb + acc_row(r, hl);
-                } else {
-                    bsec = fmaxf(bsec, z);
+            for (int r = 0; r < 16; ++r) zz[16 * mb + r] = acc[mb][nb][r];
+        if (ep.cap > 0.0f) softcap_values<32>(zz, sc, ep.cap);
+        bool may_ninf = !full_tile;  // some value may be -inf (padding, ban, a -inf bias)
+        if constexpr (META) {
+            const uint32_t* mwv = meta.w[wave][32u * nb + l32];
+            const uint32_t has_mods = col_ok ? meta.r[32u * nb + l32][0] : 0u;
+            const uint32_t hb0 = mwv[0], hb1 = mwv[1], ban0 = mwv[2], ban1 = mwv[3];
+            if (has_mods) {
+                DevRow row{};
+                row.repetition_penalty = __uint_as_float(meta.r[32u * nb + l32][1]);
+                row.presence_penalty = __uint_as_float(meta.r[32u * nb + l32][2]);
+                row.frequency_penalty = __uint_as_float(meta.r[32u * nb + l32][3]);
+                // bias first (the order of apply_entry): entries are unique per id, each read
+                // once and added to the one value that holds its id, if this lane holds it
+                if ((has_mods & 2u) && ep.block_start) {
+                    const ModEntry* me = ep.mods + (size_t)bq * ep.mod_cap;
+                    for (uint32_t k = mwv[4]; k < mwv[5]; ++k) {
+                        const ModEntry t = me[k];
+                        const uint32_t rr = t.id - base;
+#pragma unroll
+                        for (int i = 0; i < 32; ++i)
+                            if (rr == 32u * (i >> 4) + acc_row(i & 15, hl)) {
+#pragma clang fp contract(off)
+                                zz[i] = zz[i] + t.bias;
+                            }
+                    }
+                    may_ninf = true;
                 }
-                if (z != -INFINITY) bmin = fminf(bmin, z);
-            }
-        bmin = fminf(bmin, xor32(bmin));
-        // Logits: with four column blocks (B = 256) the activation buffer is free after the main
-        // loop, and each wave transposes its 64 x 32 tile through its own 8.5 KiB of it, so that
-        // one float4 store covers four whole 256-byte row segments instead of 16 bytes of 32
-        // rows. Otherwise (and for partial tiles or columns) the values leave as they lie.
-        if (kTransposeStores && ep.logits && full_tile && vec_ok && cbase + 32u * nb + 32u <= B) {
-            float* tl = epi_tl;
+                // history counts: every count of a 32-row half is loaded before any is used,
+                // then zeroed for the next step and applied; the low half of the column zeroes
+                // the tile's two bitmap words
+                if ((has_mods & 1u) && ep.hcount && (hb0 | hb1) != 0u) {
+                    uint32_t* hrow = ep.hcount + (size_t)bq * ep.V + base;
+                    if (hl == 0u) {
+                        uint32_t* hw = ep.hbits + (size_t)bq * ep.hbw + 2u * tile;
+                        if (hb0) hw[0] = 0u;
+                        if (hb1) hw[1] = 0u;
+                    }
 #pragma unroll
-            for (int mb = 0; mb < 2; ++mb)
+                    for (int mb = 0; mb < 2; ++mb) {
+                        const uint32_t hb = mb ? hb1 : hb0;
+                        if (hb == 0u) continue;
+                        uint32_t cnt[16];
 #pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    *reinterpret_cast<float4*>(tl + l32 * kTrRow + 32u * mb + 8u * q + 4u * hl) =
-                        make_float4(acc[mb][nb][4 * q], acc[mb][nb][4 * q + 1], acc[mb][nb][4 * q + 2],
-                                    acc[mb][nb][4 * q + 3]);
-            const uint32_t c0 = lane >> 4, r4 = 4u * (lane & 15u);
+                        for (int r = 0; r < 16; ++r) {
+                            const uint32_t rr = 32u * mb + acc_row(r, hl);
+                            cnt[r] = ((hb >> (rr & 31u)) & 1u) ? hrow[rr] : 0u;
+                        }
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint32_t c = 4u * (uint32_t)i + c0;  // column of the tile
-                const float4 v = *reinterpret_cast<const float4*>(tl + c * kTrRow + r4);
-                *reinterpret_cast<float4*>(ep.logits + (size_t)(cbase + 32u * nb + c) * ep.V + base + r4) = v;
-            }
-        } else if (col_ok && ep.logits) {
-            float* lrow = ep.logits + (size_t)bq * ep.V + base;
-#pragma unroll
-            for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const uint32_t rr = 32u * mb + 8u * q + 4u * hl;
-                    if (vec_ok && base + rr + 3u < ep.V) {
-                        *reinterpret_cast<float4*>(lrow + rr) =
-                            make_float4(acc[mb][nb][4 * q], acc[mb][nb][4 * q + 1],
-                                        acc[mb][nb][4 * q + 2], acc[mb][nb][4 * q + 3]);
-                    } else {
-#pragma unroll
-                        for (int t = 0; t < 4; ++t)
-                            if (base + rr + t < ep.V) lrow[rr + t] = acc[mb][nb][4 * q + t];
+                        for (int r = 0; r < 16; ++r)
+                            if (cnt[r]) {
+                                const uint32_t rr = 32u * mb + acc_row(r, hl);
+                                hrow[rr] = 0u;
+                                zz[16 * mb + r] = apply_entry(zz[16 * mb + r], ModEntry{base + rr, cnt[r], 0.0f, 0u}, row,
+                                                              ep.rep_limit);
+                            }
                     }
                 }
+            }
+            if (col_ok && ep.ban && (ban0 | ban1) != 0u) {
+#pragma unroll
+                for (int i = 0; i < 32; ++i) {
+                    const uint32_t rr = 32u * (i >> 4) + acc_row(i & 15, hl);
+                    if ((((i < 16) ? ban0 : ban1) >> (rr & 31u)) & 1u) zz[i] = -INFINITY;
+                }
+                may_ninf = true;
+            }
         }
-        const float om = xor32(bmax);
-        const uint32_t oa = xor32(barg);
-        // second largest of the two halves together: the smaller maximum or the larger second
-        bsec = fmaxf(fmaxf(bsec, xor32(bsec)), fminf(bmax, om));
-        if (om > bmax || (om == bmax && oa < barg)) { bmax = om; barg = oa; }
+        if (!full_tile) {
+#pragma unroll
+            for (int i = 0; i < 32; ++i)
+                if (base + 32u * (i >> 4) + acc_row(i & 15, hl) >= ep.V) zz[i] = -INFINITY;
+        }
+        // Block statistics over the 64 rows: the lane's 32 values, then the other half of the
+        // column (lane ^ 32).
+        float lmax, lsec = -INFINITY;
+        if (!ep.no_smax) {
+            // running maximum and second maximum (repeats count), two values at a time
+            lmax = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 32; i += 2) {
+                const float hi = fmaxf(zz[i], zz[i + 1]), lo = fminf(zz[i], zz[i + 1]);
+                lsec = fmaxf(fmaxf(lsec, lo), fminf(lmax, hi));
+                lmax = fmaxf(lmax, hi);
+            }
+        } else {
+            lmax = zz[0];
+#pragma unroll
+            for (int i = 1; i < 32; ++i) lmax = fmaxf(lmax, zz[i]);
+        }
+        const float om = xor32(lmax);
+        const float bm = fmaxf(lmax, om);  // the block maximum
+        // lowest row of the lane holding it, then the lower of the two halves' ids
+        uint32_t ri = 32u;
+#pragma unroll
+        for (int i = 31; i >= 0; --i) ri = (zz[i] == bm) ? (uint32_t)i : ri;
+        uint32_t barg = (ri < 32u) ? base + 32u * (ri >> 4) + acc_row((int)(ri & 15u), hl) : 0xFFFFFFFFu;
+        barg = min(barg, xor32(barg));
+        float bsec = -INFINITY;
+        if (!ep.no_smax) bsec = fmaxf(fmaxf(lsec, xor32(lsec)), fminf(lmax, om));
+        float bmin;
+        if (may_ninf) {
+            bmin = INFINITY;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) bmin = fminf(bmin, zz[i] == -INFINITY ? INFINITY : zz[i]);
+        } else {
+            bmin = zz[0];
+#pragma unroll
+            for (int i = 1; i < 32; ++i) bmin = fminf(bmin, zz[i]);
+        }
+        bmin = fminf(bmin, xor32(bmin));
         float se = 0.0f;
-        if (bmax != -INFINITY && !ep.no_sumexp) {
-            const float mb2 = bmax * 1.4426950408889634f;
+        if (!ep.no_sumexp) {
+            if (bm != -INFINITY) {
+                const float mb2 = bm * 1.4426950408889634f;
 #pragma unroll
-            for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    se += __builtin_amdgcn_exp2f(fmaf(acc[mb][nb][r], 1.4426950408889634f, -mb2));
+                for (int i = 0; i < 32; ++i) se += __builtin_amdgcn_exp2f(fmaf(zz[i], 1.4426950408889634f, -mb2));
+            }
+            se += xor32(se);
         }
-        se += xor32(se);
         if (col_ok && hl == 0u) {
             BlockPartial bp;
-            bp.max = bmax;
-            bp.arg = (bmax == -INFINITY) ? base : barg;
+            bp.max = bm;
+            bp.arg = (bm == -INFINITY) ? base : barg;
             bp.sumexp = se;
             bp.minf = bmin;
             bp.smax = bsec;
             ep.partials[(size_t)bq * ep.ntile + tile] = bp;
+        }
+        // Logits: each 32-row half goes through the wave's own LDS tile (32 columns x 32 rows,
+        // 16-byte pieces XOR-swizzled so that neither side conflicts), so one float4 store
+        // writes four contiguous rows of one column and 8 lanes cover a 128-byte row segment.
+        if (ep.logits) {
+            if (full_tile && vec_ok) {
+                const uint32_t rc = lane >> 3, k = lane & 7u;
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const uint32_t piece = (2u * q + hl) ^ ((l32 >> 1) & 7u);
+                        *reinterpret_cast<float4*>(tr + 32u * l32 + 4u * piece) =
+                            make_float4(zz[16 * mb + 4 * q], zz[16 * mb + 4 * q + 1], zz[16 * mb + 4 * q + 2],
+                                        zz[16 * mb + 4 * q + 3]);
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t c = 8u * (uint32_t)i + rc;  // column of the tile
+                        const float4 v = *reinterpret_cast<const float4*>(tr + 32u * c + 4u * (k ^ ((c >> 1) & 7u)));
+                        if (cbase + 32u * nb + c < B)
+                            *reinterpret_cast<float4*>(ep.logits + (size_t)(cbase + 32u * nb + c) * ep.V + base +
+                                                       32u * mb + 4u * k) = v;
+                    }
+                }
+            } else if (col_ok) {
+                float* lrow = ep.logits + (size_t)bq * ep.V + base;
+#pragma unroll
+                for (int i = 0; i < 32; ++i) {
+                    const uint32_t rr = 32u * (i >> 4) + acc_row(i & 15, hl);
+                    if (base + rr < ep.V) lrow[rr] = zz[i];
+                }
+            }
         }
     };
     [&]<int... I>(std::integer_sequence<int, I...>) {
@@ -380,26 +480,32 @@ void launch_head_mfma(const Head& h, int batch, const EpiArgs& ep, hipStream_t s
     const uint32_t ncol = 32u * (uint32_t)nb;
     const uint32_t ntg = (h.ntile + 3u) / 4u, ncb = (B + ncol - 1u) / ncol;
     const dim3 grid(ncb * ((ntg + 7u) / 8u) * 8u);
-    const bool full = (B % ncol) == 0u;
-    const bool pf2 = (h.G % 2u) == 0u;
-#define TDT_LAUNCH(NB, PF, OCC, FULL, DN)                                                           \
-    hipExtLaunchKernelGGL((k_head_mfma<NB, PF, OCC, FULL, DN>), grid, dim3(256), 0, st, ev0, ev1, 0, h.Wt, \
+    const bool meta = ep.meta != 0u;
+    // Prefetch depth: four groups when the group count allows it, else two, else one.
+    const int pf = (h.G % 4u == 0u) ? 4 : (h.G % 2u == 0u) ? 2 : 1;
+#define TDT_LAUNCH(NB, PF, OCC, DN, MT)                                                                  \
+    hipExtLaunchKernelGGL((k_head_mfma<NB, PF, OCC, DN, MT>), grid, dim3(256), 0, st, ev0, ev1, 0, h.Wt, \
                           h.SB16t, h.x16, B, h.D, h.NC, h.G, ncb, ntg, ep)
-#define TDT_PICK2(NB, OCC, DN)                                                                     \
-    do {                                                                                           \
-        if (pf2) { if (full) TDT_LAUNCH(NB, 2, OCC, true, DN); else TDT_LAUNCH(NB, 2, OCC, false, DN); } \
-        else { if (full) TDT_LAUNCH(NB, 1, OCC, true, DN); else TDT_LAUNCH(NB, 1, OCC, false, DN); }     \
+#define TDT_PICK_PF(NB, OCC, DN, MT)                               \
+    do {                                                           \
+        if (pf == 4) TDT_LAUNCH(NB, 4, OCC, DN, MT);                \
+        else if (pf == 2) TDT_LAUNCH(NB, 2, OCC, DN, MT);           \
+        else TDT_LAUNCH(NB, 1, OCC, DN, MT);                        \
     } while (0)
-#define TDT_PICK(NB, OCC)                                   \
-    do {                                                    \
-        if (h.mfma_denorm) TDT_PICK2(NB, OCC, true);        \
-        else TDT_PICK2(NB, OCC, false);                     \
+#define TDT_PICK(NB, OCC)                                                                 \
+    do {                                                                                  \
+        if (h.mfma_denorm) { if (meta) TDT_PICK_PF(NB, OCC, true, true); else TDT_PICK_PF(NB, OCC, true, false); } \
+        else { if (meta) TDT_PICK_PF(NB, OCC, false, true); else TDT_PICK_PF(NB, OCC, false, false); }             \
     } while (0)
-    if (nb == 1) TDT_PICK(1, 4);
-    else if (nb == 2) TDT_PICK(2, 3);
-    else TDT_PICK(4, 2);
+    if (nb == 1) {
+        TDT_PICK(1, 3);
+    } else if (nb == 2) {
+        TDT_PICK(2, 2);
+    } else {
+        TDT_PICK(4, 2);
+    }
 #undef TDT_PICK
-#undef TDT_PICK2
+#undef TDT_PICK_PF
 #undef TDT_LAUNCH
     check_hip(hipGetLastError(), "head (MFMA)");
 }
