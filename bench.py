@@ -49,7 +49,7 @@ WEIGHT_BYTES = V * D // 2 + 2 * (V * (D // 64) * 2)  # 415,236,096
 HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFLOPS = 2500.0  # dense bf16 / fp16
 METRIC = "LM-head+sample tokens/sec at B=1/32/256; % HBM roofline (B=1), % MFMA (B=256)"
-TRAFFIC_FILE = ROOT / "profiles" / "head_b1_traffic.json"
+TRAFFIC_FILE = ROOT / "profiles" / "head_traffic.json"
 CPU_THREADS_CAP = 16
 
 
@@ -74,14 +74,14 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def head_kernel_name(B: int) -> str:
-    """The head kernel the library launches for a batch of B rows over this head's shape."""
+def head_kernel_name(B: int, meta: bool) -> str:
+    """The head kernel the library launches for a batch of B rows over this head's shape (group
+    count divisible by 4, every scale below 1/16); meta: some row has modifiers or a ban mask."""
     if B <= 2:
         return f"k_head_digits_fused<{B}>"
     nb = 1 if B <= 32 else 2 if B <= 64 else 4
-    occ = {1: 4, 2: 3, 4: 2}[nb]
-    full = "true" if B % (32 * nb) == 0 else "false"
-    return f"k_head_mfma<{nb}, 2, {occ}, {full}>"
+    occ = {1: 3, 2: 2, 4: 2}[nb]
+    return f"k_head_mfma<{nb}, 4, {occ}, true, {'true' if meta else 'false'}>"
 
 
 class Workload:
@@ -255,7 +255,7 @@ def measure(torch, head, wl, warmup, steps, tsteps, first=0):
         "unit": "TFLOP/s" if bound == "mfma" else "GB/s",
         "frac": (tfl / MFMA_PEAK_TFLOPS) if bound == "mfma" else (gbs / HBM_PEAK_GBS),
         "traffic": None,
-        "kernel": head_kernel_name(wl.B), "kernel_avg_us": 1e3 * kavg, "timed_launches": n,
+        "kernel": head_kernel_name(wl.B, wl.B in (32, 64)), "kernel_avg_us": 1e3 * kavg, "timed_launches": n,
         "algorithmic_bytes_per_launch": nbytes, "algorithmic_flops_per_launch": flops,
         "hbm_GBs": gbs, "hbm_frac": gbs / HBM_PEAK_GBS, "TFLOPs": tfl, "mfma_frac": tfl / MFMA_PEAK_TFLOPS,
     }
@@ -411,7 +411,9 @@ def main():
         batched = []
     for Bn in batched:
         log(f"B={Bn}")
-        st = max(a.steps // 4, 16) if Bn == 256 else max(a.steps // 2, 16)
+        # at least 64 timed steps per batched line, whatever --steps is: the first steps of a
+        # workload carry one-time costs that a handful of steps would not amortise
+        st = max(a.steps // 4, 64) if Bn == 256 else max(a.steps // 2, 64)
         lines[f"b{Bn}"] = measure(torch, head, Batched(T, torch, head, Bn), max(a.warmup, 3), st,
                                   min(tsteps, 32))
     head.close()
@@ -420,12 +422,18 @@ def main():
         print(json.dumps({"only": a.only, **res}), flush=True)
         return
 
-    traffic = None
+    # HBM bytes per head launch from the committed counter summary (FETCH_SIZE + WRITE_SIZE, each
+    # calibrated on a copy kernel); workloads without a counter pass keep null
+    measured = {}
     if TRAFFIC_FILE.exists():
         try:
-            traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
+            measured = {k: v.get("hbm_bytes_per_launch")
+                        for k, v in json.loads(TRAFFIC_FILE.read_text()).get("workloads", {}).items()}
         except Exception:
-            traffic = None
+            measured = {}
+    traffic = measured.get("b1")
+    for name, ln in lines.items():
+        ln["roofline"]["traffic"] = measured.get(name)
     roof = dict(main_line["roofline"])
     roof["traffic"] = traffic
     line = {
