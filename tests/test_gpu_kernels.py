@@ -178,3 +178,26 @@ def test_logits_mfma_path_large_scales(batch):
             assert U.logit_err(got[b], want) <= U.LOGIT_RTOL, b
     finally:
         h.close()
+
+
+@pytest.mark.parametrize("hidden", [2944, 2880])
+@pytest.mark.parametrize("batch", [3, 64, 130])
+def test_logits_mfma_path_other_group_counts(hidden, batch):
+    """The batched head prefetches four 64-element groups ahead when the group count allows it,
+    else two (hidden 2944: 46 groups), else one (hidden 2880: 45 groups). A vocabulary of 4099
+    rows leaves a partial last tile and rows that are not 16-byte aligned (element stores), and
+    130 rows a partial second column block."""
+    Vh = 4099
+    W, S, B, g = synth.make_head(Vh, hidden, 104)
+    h = T.LMHead(W, S, B, g, vocab=Vh, hidden=hidden)
+    try:
+        x = np.stack([O.rms_norm(r, g, 1e-6) for r in synth.hidden_states(batch, hidden, 9)])
+        out = torch.empty((batch, Vh), dtype=torch.float32, device="cuda")
+        h.logits(dev(x), batch, out)
+        h.sync()
+        got = out.cpu().numpy()
+        for b in sorted({0, batch // 2, batch - 1}):
+            want = O.softcap(O.matvec(W, S, B, x[b], U.THREADS), 30.0)
+            assert U.logit_err(got[b], want) <= U.LOGIT_RTOL, b
+    finally:
+        h.close()
