@@ -225,50 +225,59 @@ __device__ void prep_row(const PrepArgs& a, uint32_t b, uint32_t k) {
     }
 }
 
-__device__ void modtable_row(const PrepArgs& a, uint32_t b, unsigned long long* keys) {
+// Row b's history occurrence counts into the dense hcount / hbits arrays.
+__device__ void history_counts(const PrepArgs& a, uint32_t b, unsigned long long* keys) {
+    const uint32_t tid = threadIdx.x;
+    const uint32_t V = a.V;
+    // One count per occurrence (src/sampling.cpp:81-89 visits every occurrence); ids past
+    // the vocabulary are ignored (:82). Occurrences are first merged per id in an LDS table
+    // (one slot per hash of the id; an occurrence whose slot holds another id goes straight
+    // to the global counters), so a frequent id costs one global atomic instead of one per
+    // occurrence: same-address global atomics serialise in L2.
+    uint32_t* hk = reinterpret_cast<uint32_t*>(keys);  // [kHistSlots] ids, ~0 when empty
+    uint32_t* hc = hk + kHistSlots;                     // [kHistSlots] occurrence counts
+    for (uint32_t i = tid; i < kHistSlots; i += kPrepThreads) {
+        hk[i] = ~0u;
+        hc[i] = 0u;
+    }
+    __syncthreads();
+    const uint32_t nh = min(a.hist_len[b], a.hist_stride);
+    const uint32_t* hist = a.history + (size_t)b * a.hist_stride;
+    for (uint32_t i = tid; i < nh; i += kPrepThreads) {
+        const uint32_t id = hist[i];
+        if (id < V) {
+            const uint32_t slot = (id * 2654435761u) >> (32u - kHistSlotBits);
+            const uint32_t prev = atomicCAS(&hk[slot], ~0u, id);
+            if (prev == ~0u || prev == id) {
+                atomicAdd(&hc[slot], 1u);
+            } else {
+                atomicAdd(a.hcount + (size_t)b * V + id, 1u);
+                atomicOr(a.hbits + (size_t)b * a.hbw + (id >> 5), 1u << (id & 31u));
+            }
+        }
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < kHistSlots; i += kPrepThreads) {
+        const uint32_t id = hk[i];
+        if (id != ~0u) {
+            atomicAdd(a.hcount + (size_t)b * V + id, hc[i]);
+            atomicOr(a.hbits + (size_t)b * a.hbw + (id >> 5), 1u << (id & 31u));
+        }
+    }
+}
+
+// part 0: row b's history counts; part 1: row b's bias table (independent outputs, so the two
+// run in separate blocks at the same time).
+__device__ void modtable_row(const PrepArgs& a, uint32_t b, unsigned long long* keys, uint32_t part) {
 #pragma clang fp contract(off)
     __shared__ uint32_t s_scan[kPrepWaves];
     __shared__ uint32_t s_nruns;
     const uint32_t tid = threadIdx.x;
     const uint32_t use = (a.mod_bits[b >> 4] >> (2u * (b & 15u))) & 3u;
     const uint32_t V = a.V;
-    if ((use & 1u) && a.history) {
-        // One count per occurrence (src/sampling.cpp:81-89 visits every occurrence); ids past
-        // the vocabulary are ignored (:82). Occurrences are first merged per id in an LDS table
-        // (one slot per hash of the id; an occurrence whose slot holds another id goes straight
-        // to the global counters), so a frequent id costs one global atomic instead of one per
-        // occurrence: same-address global atomics serialise in L2.
-        uint32_t* hk = reinterpret_cast<uint32_t*>(keys);  // [kHistSlots] ids, ~0 when empty
-        uint32_t* hc = hk + kHistSlots;                     // [kHistSlots] occurrence counts
-        for (uint32_t i = tid; i < kHistSlots; i += kPrepThreads) {
-            hk[i] = ~0u;
-            hc[i] = 0u;
-        }
-        __syncthreads();
-        const uint32_t nh = min(a.hist_len[b], a.hist_stride);
-        const uint32_t* hist = a.history + (size_t)b * a.hist_stride;
-        for (uint32_t i = tid; i < nh; i += kPrepThreads) {
-            const uint32_t id = hist[i];
-            if (id < V) {
-                const uint32_t slot = (id * 2654435761u) >> (32u - kHistSlotBits);
-                const uint32_t prev = atomicCAS(&hk[slot], ~0u, id);
-                if (prev == ~0u || prev == id) {
-                    atomicAdd(&hc[slot], 1u);
-                } else {
-                    atomicAdd(a.hcount + (size_t)b * V + id, 1u);
-                    atomicOr(a.hbits + (size_t)b * a.hbw + (id >> 5), 1u << (id & 31u));
-                }
-            }
-        }
-        __syncthreads();
-        for (uint32_t i = tid; i < kHistSlots; i += kPrepThreads) {
-            const uint32_t id = hk[i];
-            if (id != ~0u) {
-                atomicAdd(a.hcount + (size_t)b * V + id, hc[i]);
-                atomicOr(a.hbits + (size_t)b * a.hbw + (id >> 5), 1u << (id & 31u));
-            }
-        }
-        __syncthreads();  // the bias table below reuses the pool
+    if (part == 0u) {
+        if ((use & 1u) && a.history) history_counts(a, b, keys);
+        return;
     }
     if (!(use & 2u) || !a.bias_ids) return;
     const uint32_t P = a.P;
@@ -322,26 +331,35 @@ __device__ void modtable_row(const PrepArgs& a, uint32_t b, unsigned long long* 
             total = total + a.bias_vals[(size_t)b * a.bias_stride + (uint32_t)keys[t]];
         mods[r] = ModEntry{(uint32_t)(keys[s0] >> 32), 0u, total, 1u};
     }
-    // block_start[t] = number of entries with id < 64 t: a binary search over the run ids.
+    // block_start[t] = number of entries with id < 64 t. Each thread covers a contiguous range of
+    // tiles: one binary search over the run ids for its first tile, then a walk upwards (the ids
+    // are sorted).
     const uint32_t ntile = a.ntile;
     uint32_t* bs = a.block_start + (size_t)b * (ntile + 1u);
-    for (uint32_t t = tid; t <= ntile; t += kPrepThreads) {
-        const uint32_t target = t * kTileRows;
+    const uint32_t tper = (ntile + 1u + kPrepThreads - 1u) / kPrepThreads;
+    const uint32_t t0 = tid * tper;
+    if (t0 <= ntile) {
         uint32_t lo = 0, hi = nruns;
         while (lo < hi) {
             const uint32_t mid = (lo + hi) >> 1;
-            if ((uint32_t)(keys[rs[mid]] >> 32) < target) lo = mid + 1u;
+            if ((uint32_t)(keys[rs[mid]] >> 32) < t0 * kTileRows) lo = mid + 1u;
             else hi = mid;
         }
-        bs[t] = lo;
+        for (uint32_t t = t0; t < t0 + tper && t <= ntile; ++t) {
+            while (lo < nruns && (uint32_t)(keys[rs[lo]] >> 32) < t * kTileRows) ++lo;
+            bs[t] = lo;
+        }
     }
     if (tid == 0u) a.mod_count[b] = nruns;
 }
 
 // Grid: [row copy block if rows_dst] [B x ceil(D / 1024) RMSNorm blocks if hidden]
-// [B table blocks if mods].
+// [B history blocks, then B bias-table blocks, if mods].
 __global__ __launch_bounds__(kPrepThreads) void k_step_prep(PrepArgs a) {
-    __shared__ unsigned long long pool[kPrepPoolU64];
+    // The modifier blocks' table (history merge, then bias keys and run starts), sized per launch:
+    // dynamic, so that launches without modifiers, or with small bias lists, fit several blocks
+    // per CU.
+    extern __shared__ unsigned long long pool[];
     uint32_t blk = blockIdx.x;
     if (a.rows_dst) {
         if (blk == 0u) {
@@ -364,16 +382,29 @@ __global__ __launch_bounds__(kPrepThreads) void k_step_prep(PrepArgs a) {
         }
         blk -= (uint32_t)a.B * per;
     }
-    modtable_row(a, blk, pool);
+    modtable_row(a, blk % (uint32_t)a.B, pool, blk / (uint32_t)a.B);
 }
 
 void launch_step_prep(const Head& h, const PrepArgs& a, bool with_mods, hipStream_t st) {
-    // The pool holds kModCap keys + run starts (P <= mod_cap) for the bias-table blocks.
     const unsigned per = (a.D + kPrepThreads - 1u) / kPrepThreads;
     const unsigned grid = (a.rows_dst ? 1u : 0u) + (a.hidden ? (unsigned)a.B * per : 0u) +
-                          (with_mods ? (unsigned)a.B : 0u);
+                          (with_mods ? 2u * (unsigned)a.B : 0u);
     if (grid == 0u) return;
-    hipLaunchKernelGGL(k_step_prep, dim3(grid), dim3(kPrepThreads), 0, st, a);
+    // LDS for the modifier blocks: the history table (kHistSlots ids + counts) or P bias keys and
+    // P + 1 run starts (P <= mod_cap), whichever is larger; none without modifiers.
+    size_t lds = 0;
+    if (with_mods) {
+        const size_t hist = 2u * kHistSlots * sizeof(uint32_t);
+        const size_t bias = (size_t)a.P * sizeof(unsigned long long) + ((size_t)a.P + 2u) * sizeof(uint32_t);
+        lds = (std::max(hist, bias) + 15u) & ~(size_t)15u;
+    }
+    if (lds > 65536u) {
+        static_assert(kPrepPoolU64 * 8u <= 160u * 1024u, "the largest table must fit one CU's LDS");
+        check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(k_step_prep),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+                  "step prep LDS size");
+    }
+    hipLaunchKernelGGL(k_step_prep, dim3(grid), dim3(kPrepThreads), lds, st, a);
     check_hip(hipGetLastError(), "step prep");
 }
 
