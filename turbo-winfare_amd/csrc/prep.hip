@@ -282,12 +282,14 @@ __device__ void modtable_row(const PrepArgs& a, uint32_t b, unsigned long long* 
     if (!(use & 2u) || !a.bias_ids) return;
     const uint32_t P = a.P;
     uint32_t* rs = reinterpret_cast<uint32_t*>(keys + P);  // run starts, [nruns + 1] <= P + 1
+    float* vals = reinterpret_cast<float*>(rs + P + 2u);    // the list's values, by position
     const uint32_t nb = min(a.bias_count[b], a.bias_stride);
     const unsigned long long kPad = ~0ull;
     for (uint32_t i = tid; i < P; i += kPrepThreads) {
         unsigned long long k = kPad;
         if (i < nb) {
             const uint32_t id = a.bias_ids[(size_t)b * a.bias_stride + i];
+            vals[i] = a.bias_vals[(size_t)b * a.bias_stride + i];  // loaded beside the id
             if (id < V) k = ((unsigned long long)id << 32) | i;
         }
         keys[i] = k;
@@ -327,8 +329,7 @@ __device__ void modtable_row(const PrepArgs& a, uint32_t b, unsigned long long* 
     for (uint32_t r = tid; r < nruns; r += kPrepThreads) {
         const uint32_t s0 = rs[r], s1 = rs[r + 1u];
         float total = 0.0f;
-        for (uint32_t t = s0; t < s1; ++t)
-            total = total + a.bias_vals[(size_t)b * a.bias_stride + (uint32_t)keys[t]];
+        for (uint32_t t = s0; t < s1; ++t) total = total + vals[(uint32_t)keys[t]];
         mods[r] = ModEntry{(uint32_t)(keys[s0] >> 32), 0u, total, 1u};
     }
     // block_start[t] = number of entries with id < 64 t. Each thread covers a contiguous range of
@@ -390,16 +391,17 @@ void launch_step_prep(const Head& h, const PrepArgs& a, bool with_mods, hipStrea
     const unsigned grid = (a.rows_dst ? 1u : 0u) + (a.hidden ? (unsigned)a.B * per : 0u) +
                           (with_mods ? 2u * (unsigned)a.B : 0u);
     if (grid == 0u) return;
-    // LDS for the modifier blocks: the history table (kHistSlots ids + counts) or P bias keys and
-    // P + 1 run starts (P <= mod_cap), whichever is larger; none without modifiers.
+    // LDS for the modifier blocks: the history table (kHistSlots ids + counts) or P bias keys,
+    // P + 1 run starts and P values (P <= mod_cap), whichever is larger; none without modifiers.
     size_t lds = 0;
     if (with_mods) {
         const size_t hist = 2u * kHistSlots * sizeof(uint32_t);
-        const size_t bias = (size_t)a.P * sizeof(unsigned long long) + ((size_t)a.P + 2u) * sizeof(uint32_t);
+        const size_t bias = (size_t)a.P * sizeof(unsigned long long) + ((size_t)a.P + 2u) * sizeof(uint32_t) +
+                            (size_t)a.P * sizeof(float);
         lds = (std::max(hist, bias) + 15u) & ~(size_t)15u;
     }
     if (lds > 65536u) {
-        static_assert(kPrepPoolU64 * 8u <= 160u * 1024u, "the largest table must fit one CU's LDS");
+        static_assert(kModCap * 16u + 16u <= 160u * 1024u, "the largest table must fit one CU's LDS");
         check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(k_step_prep),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
                   "step prep LDS size");
