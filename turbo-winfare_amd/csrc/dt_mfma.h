@@ -178,4 +178,16 @@ __device__ inline uint32_t acc_row(int r, uint32_t hl) { return 8u * (uint32_t)(
 
 __device__ inline uint32_t word_of(const uint4& w, int j) { return (j == 0) ? w.x : (j == 1) ? w.y : (j == 2) ? w.z : w.w; }
 
+// Issue priority by progress: 3 in the first quarter of the G groups, down to 0 in the last.
+// The SIMD arbiter otherwise favours the oldest waves, so workgroups that share a CU finish one
+// after another and the last runs alone with a fraction of the CU's loads in flight; lowering
+// the priority of the waves ahead lets the others catch up, and they finish together.
+__device__ inline void prio_by_progress(uint32_t g, uint32_t G) {
+    const uint32_t q = (4u * g) / G;
+    if (q == 0u) __builtin_amdgcn_s_setprio(3);
+    else if (q == 1u) __builtin_amdgcn_s_setprio(2);
+    else if (q == 2u) __builtin_amdgcn_s_setprio(1);
+    else __builtin_amdgcn_s_setprio(0);
+}
+
 }  // namespace tdt

@@ -16,9 +16,9 @@
 //    to match the order the dequant produces halves in.
 //  * Workgroup = 4 waves, one 64-row tile each, over a block of 32*NB batch columns
 //    (B = 256 runs two column blocks, on the same XCD back to back so the second reads the
-//    weights from L2). Weights and activations are prefetched PF
-//    groups ahead into registers; the activations of group g+1 are written into the other half
-//    of a double-buffered LDS tile at the end of group g, one barrier per group.
+//    weights from L2). Weights and scales are prefetched PF groups ahead into registers by
+//    buffer loads; the activations reach a ring in LDS by buffer-to-LDS DMA, PF - 1 groups
+//    ahead, with one wait and one barrier per group.
 //  * Epilogue in place on the accumulators: per (column, 64-row tile), lane-local reductions
 //    and one cross-lane exchange give the block partial; logits leave as float4 stores.
 #include <hip/hip_ext.h>
@@ -210,6 +210,12 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
 #pragma unroll
         for (int p = 0; p < PF; ++p) {
             const uint32_t g = g0 + p;
+            // Up to 64 columns every workgroup is resident from the start (four per CU): even
+            // progress keeps all four streaming until the end (B = 32 head 94 -> 89 us, B = 64
+            // 141 -> 135 us). With four column blocks the workgroups come in rounds, and the
+            // staggered ends that age order gives overlap one round's epilogues with the next
+            // round's loop (there the priorities measured 12 us slower).
+            if constexpr (NB <= 2) prio_by_progress(g, G);
             // stage of group g; group g + PF - 1 goes to the stage group g - 1 used (every wave
             // finished with it before the last barrier)
             const uint32_t st = (PF > 1) ? (uint32_t)p : (g & 1u);
@@ -481,31 +487,40 @@ void launch_head_mfma(const Head& h, int batch, const EpiArgs& ep, hipStream_t s
     const uint32_t ntg = (h.ntile + 3u) / 4u, ncb = (B + ncol - 1u) / ncol;
     const dim3 grid(ncb * ((ntg + 7u) / 8u) * 8u);
     const bool meta = ep.meta != 0u;
-    // Prefetch depth: four groups when the group count allows it, else two, else one.
+    // Prefetch depth: four groups when the group count allows it, else two, else one. Two column
+    // blocks run at four workgroups per CU (all 1024 of a 262,144-row head resident at once, where
+    // three per CU left a second round of 256 running alone) and hold two groups, which fits the
+    // 128 registers that occupancy allows.
     const int pf = (h.G % 4u == 0u) ? 4 : (h.G % 2u == 0u) ? 2 : 1;
 #define TDT_LAUNCH(NB, PF, OCC, DN, MT)                                                                  \
     hipExtLaunchKernelGGL((k_head_mfma<NB, PF, OCC, DN, MT>), grid, dim3(256), 0, st, ev0, ev1, 0, h.Wt, \
                           h.SB16t, h.x16, B, h.D, h.NC, h.G, ncb, ntg, ep)
-#define TDT_PICK_PF(NB, OCC, DN, MT)                               \
+#define TDT_PF421(NB, OCC, DN, MT)                                 \
     do {                                                           \
         if (pf == 4) TDT_LAUNCH(NB, 4, OCC, DN, MT);                \
         else if (pf == 2) TDT_LAUNCH(NB, 2, OCC, DN, MT);           \
         else TDT_LAUNCH(NB, 1, OCC, DN, MT);                        \
     } while (0)
-#define TDT_PICK(NB, OCC)                                                                 \
+#define TDT_PF21(NB, OCC, DN, MT)                                  \
+    do {                                                           \
+        if (pf >= 2) TDT_LAUNCH(NB, 2, OCC, DN, MT);                \
+        else TDT_LAUNCH(NB, 1, OCC, DN, MT);                        \
+    } while (0)
+#define TDT_PICK(NB, OCC, PFS)                                                            \
     do {                                                                                  \
-        if (h.mfma_denorm) { if (meta) TDT_PICK_PF(NB, OCC, true, true); else TDT_PICK_PF(NB, OCC, true, false); } \
-        else { if (meta) TDT_PICK_PF(NB, OCC, false, true); else TDT_PICK_PF(NB, OCC, false, false); }             \
+        if (h.mfma_denorm) { if (meta) PFS(NB, OCC, true, true); else PFS(NB, OCC, true, false); } \
+        else { if (meta) PFS(NB, OCC, false, true); else PFS(NB, OCC, false, false); }             \
     } while (0)
     if (nb == 1) {
-        TDT_PICK(1, 3);
+        TDT_PICK(1, 3, TDT_PF421);
     } else if (nb == 2) {
-        TDT_PICK(2, 2);
+        TDT_PICK(2, 4, TDT_PF21);
     } else {
-        TDT_PICK(4, 2);
+        TDT_PICK(4, 2, TDT_PF421);
     }
 #undef TDT_PICK
-#undef TDT_PICK_PF
+#undef TDT_PF21
+#undef TDT_PF421
 #undef TDT_LAUNCH
     check_hip(hipGetLastError(), "head (MFMA)");
 }
