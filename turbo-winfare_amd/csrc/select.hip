@@ -435,40 +435,58 @@ __device__ __attribute__((always_inline)) inline int find_cross(SelShared& s, co
 
 // ---- full-vocabulary path on value bins ------------------------------------------------------------
 
-// Bins [0, limit) of h scanned from bin 0: the bin where the running weight first reaches
-// target. Returns 1 with bin/above; 0 with *above = the total of the range otherwise.
+// Weight-histogram scan from bin 0 up over bins [0, limit) of h (kVBins u64 fixed-point
+// weights): the bin where the running total first reaches target (before < target <= before +
+// h[bin]). Returns 1 with bin and the weight before it, or 0 with the total when target exceeds
+// it. Wave 0 does all of it (32 bins per lane, exact integer running sums, then the 32 bins of
+// the crossing lane one per lane) while the other waves wait at one barrier: a block-wide scan
+// costs several barriers, and each phase between them issues on four waves per SIMD.
 __device__ inline int scan_cross(SelShared& s, const unsigned long long* h, uint32_t limit, double target,
                                  uint32_t* bin, double* above) {
+    constexpr uint32_t kPer = kVBins / 64u;
+    static_assert(kPer <= 64u, "the crossing lane's bins are resolved one per lane");
     const uint32_t tid = threadIdx.x;
-    const uint32_t per = kVBins / sel_nt();
-    double loc = 0.0;
-    for (uint32_t j = 0; j < per; ++j) {
-        const uint32_t bi = tid * per + j;
-        if (bi < limit) loc += (double)h[bi] / kFx;
-    }
-    double tot;
-    double before = block_excl_scan<double>(loc, s, &tot);
-    if (tid == 0) s.bu[0] = 0xFFFFFFFFu;
-    __syncthreads();
-    for (uint32_t j = 0; j < per; ++j) {
-        const uint32_t bi = tid * per + j;
-        const double hv = (bi < limit) ? (double)h[bi] / kFx : 0.0;
-        if (hv > 0.0 && before < target && target <= before + hv) {
-            s.bu[0] = bi;
-            s.bd[0] = before;
+    auto fx = [](unsigned long long v) { return (double)v / kFx; };
+    if (tid < 64u) {
+        const uint32_t b0 = tid * kPer;
+        unsigned long long loc = 0ull;
+#pragma unroll 8
+        for (uint32_t j = 0; j < kPer; ++j) loc += (b0 + j < limit) ? h[b0 + j] : 0ull;
+        const unsigned long long incl = wave_incl_scan(loc, tid), run = incl - loc;
+        const unsigned long long hit = __ballot(loc != 0ull && fx(run) < target && target <= fx(incl));
+        if (hit == 0ull) {
+            if (tid == 0u) {
+                s.bu[0] = 0xFFFFFFFFu;
+                s.bd[0] = fx(lane_read(incl, 63));
+            }
+        } else {
+            // the crossing lane's bins, bin j on lane j: exclusive sums from the lane's start
+            const uint32_t L = (uint32_t)__ffsll((long long)hit) - 1u;
+            const unsigned long long base = lane_read(run, (int)L);
+            const uint32_t bj = L * kPer + (tid & (kPer - 1u));
+            const unsigned long long hv = (tid < kPer && bj < limit) ? h[bj] : 0ull;
+            const unsigned long long ci = base + wave_incl_scan(hv, tid), ce = ci - hv;
+            // the first such bin exists: the sums are monotone and the lane's range holds target
+            const unsigned long long at = __ballot(hv != 0ull && fx(ce) < target && target <= fx(ci));
+            if (at != 0ull) {
+                const uint32_t F = (uint32_t)__ffsll((long long)at) - 1u;
+                if (tid == F) {
+                    s.bu[0] = bj;
+                    s.bd[0] = fx(ce);
+                }
+            } else if (tid == 0u) {  // unreachable by the argument above; never leave a stale answer
+                s.bu[0] = min(L * kPer + kPer - 1u, limit - 1u);
+                s.bd[0] = fx(base);
+            }
         }
-        before += hv;
     }
     __syncthreads();
     const uint32_t r = s.bu[0];
     const double ab = s.bd[0];
     __syncthreads();
-    if (r == 0xFFFFFFFFu) {
-        *above = tot;
-        return 0;
-    }
-    *bin = r;
     *above = ab;
+    if (r == 0xFFFFFFFFu) return 0;
+    *bin = r;
     return 1;
 }
 
