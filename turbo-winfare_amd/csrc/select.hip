@@ -624,6 +624,34 @@ __device__ __attribute__((always_inline)) inline int fine_cross(SelShared& s, co
     const uint32_t ns = s.bu[5];
     __syncthreads();
     if (ns == 0u || ns > kSubCap) return 0;
+    if (ns <= 64u) {
+        // the usual case, in wave 0 alone: the same rank sort, scan and first crossing as the
+        // block-wide code below (one lane per element), with one barrier instead of eight. A
+        // wave's LDS accesses complete in order, so the in-place placement and the read-back
+        // need no barrier.
+        if (tid < 64u) {
+            const bool act = tid < ns;
+            const unsigned long long mine = act ? sub[tid] : 0ull;
+            uint32_t rank = 0u;
+            for (uint32_t j = 0; j < ns; ++j) rank += (sub[j] < mine) ? 1u : 0u;
+            if (act) sub[rank] = mine;
+            const unsigned long long ks = act ? sub[tid] : 0ull;
+            const double w = act ? (double)__builtin_amdgcn_exp2f((key_float(~(uint32_t)(ks >> 32)) - c.m) * kw) : 0.0;
+            const double run = wave_incl_scan(w, tid) - w;
+            const unsigned long long hit = __ballot(act && above + run + w >= target);
+            const uint32_t pick = hit ? (uint32_t)__ffsll((long long)hit) - 1u : ns - 1u;
+            if (tid == pick) {
+                s.bd[3] = above + run;
+                s.bu[6] = (uint32_t)ks;
+                s.bu[7] = (uint32_t)(ks >> 32);
+            }
+        }
+        __syncthreads();
+        *key_out = ((unsigned long long)s.bu[7] << 32) | s.bu[6];
+        *before_out = s.bd[3];
+        __syncthreads();
+        return 1;
+    }
     // rank sort of the sub-bin (distinct keys)
     unsigned long long mine = 0ull;
     uint32_t rank = 0u;
