@@ -306,11 +306,23 @@ __device__ inline uint32_t vbin(const RowCtx& c, float l) {
     const float d = (c.m - l) * c.inv_w;
     return (d < (float)(kVBins - 1)) ? (uint32_t)d : kVBins - 1u;
 }
+// The same bin from dl = l - m, which a weight needs anyway: m - l = -(l - m) and the product
+// with -inv_w round identically, so this equals vbin(c, l).
+__device__ inline uint32_t vbin_d(const RowCtx& c, float dl) {
+    const float d = dl * -c.inv_w;
+    return (d < (float)(kVBins - 1)) ? (uint32_t)d : kVBins - 1u;
+}
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// floor(w 2^40) for a weight w in [0, 1]: the integer part of a = w 2^8 is the high word and
+// that of frac(a) 2^32 the low word (both products are exact scalings), five instructions where
+// the float-to-u64 conversion takes seven, once per element of a row pass.
 __device__ inline unsigned long long to_fx(float w) {
-    return (unsigned long long)(w * 1099511627776.0f);
+    const float a = w * 256.0f;
+    const uint32_t hi = (uint32_t)a;
+    const uint32_t lo = (uint32_t)(__builtin_amdgcn_fractf(a) * 4294967296.0f);
+    return ((unsigned long long)hi << 32) | lo;
 }
 
 // Weight of logit v: mode 0 count, 1 exp(v - m), 2 exp((v - m) / T); hardware exp2.
@@ -512,8 +524,8 @@ __device__ __attribute__((always_inline)) inline void fv_hist(SelShared& s, cons
     __syncthreads();
     row_pass(c.l + beg, end - beg, [&](float v, uint32_t) {
         if (v == -INFINITY) return;
-        const uint32_t b = vbin(c, v);
         const float d = v - c.m;
+        const uint32_t b = vbin_d(c, d);
         atomicAdd(&s.vm[b], to_fx(__builtin_amdgcn_exp2f(d * kLog2e)));
         if (!same) atomicAdd(&s.vq[b], to_fx(__builtin_amdgcn_exp2f(d * kq)));
     });
