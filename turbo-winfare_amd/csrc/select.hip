@@ -448,48 +448,59 @@ __device__ __attribute__((always_inline)) inline int find_cross(SelShared& s, co
 // ---- full-vocabulary path on value bins ------------------------------------------------------------
 
 // Weight-histogram scan from bin 0 up over bins [0, limit) of h (kVBins u64 fixed-point
-// weights): the bin where the running total first reaches target (before < target <= before +
-// h[bin]). Returns 1 with bin and the weight before it, or 0 with the total when target exceeds
-// it. Wave 0 does all of it (32 bins per lane, exact integer running sums, then the 32 bins of
-// the crossing lane one per lane) while the other waves wait at one barrier: a block-wide scan
-// costs several barriers, and each phase between them issues on four waves per SIMD.
-__device__ inline int scan_cross(SelShared& s, const unsigned long long* h, uint32_t limit, double target,
-                                 uint32_t* bin, double* above) {
+// weights), by the 64 lanes of one wave: the bin where the running total first reaches target
+// (before < target <= before + h[bin]). Returns 1 with bin and the weight before it, or 0 with
+// the total when target exceeds it; every lane gets the same answer. Each lane adds 32 bins as
+// exact integers, a wave scan finds the lane whose range holds the crossing, and that lane's 32
+// bins, one per lane, find the bin.
+__device__ inline int wave_cross(const unsigned long long* h, uint32_t limit, double target, uint32_t* bin,
+                                 double* above) {
     constexpr uint32_t kPer = kVBins / 64u;
     static_assert(kPer <= 64u, "the crossing lane's bins are resolved one per lane");
-    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = threadIdx.x & 63u;
     auto fx = [](unsigned long long v) { return (double)v / kFx; };
-    if (tid < 64u) {
-        const uint32_t b0 = tid * kPer;
-        unsigned long long loc = 0ull;
+    const uint32_t b0 = lane * kPer;
+    unsigned long long loc = 0ull;
 #pragma unroll 8
-        for (uint32_t j = 0; j < kPer; ++j) loc += (b0 + j < limit) ? h[b0 + j] : 0ull;
-        const unsigned long long incl = wave_incl_scan(loc, tid), run = incl - loc;
-        const unsigned long long hit = __ballot(loc != 0ull && fx(run) < target && target <= fx(incl));
-        if (hit == 0ull) {
-            if (tid == 0u) {
-                s.bu[0] = 0xFFFFFFFFu;
-                s.bd[0] = fx(lane_read(incl, 63));
-            }
-        } else {
-            // the crossing lane's bins, bin j on lane j: exclusive sums from the lane's start
-            const uint32_t L = (uint32_t)__ffsll((long long)hit) - 1u;
-            const unsigned long long base = lane_read(run, (int)L);
-            const uint32_t bj = L * kPer + (tid & (kPer - 1u));
-            const unsigned long long hv = (tid < kPer && bj < limit) ? h[bj] : 0ull;
-            const unsigned long long ci = base + wave_incl_scan(hv, tid), ce = ci - hv;
-            // the first such bin exists: the sums are monotone and the lane's range holds target
-            const unsigned long long at = __ballot(hv != 0ull && fx(ce) < target && target <= fx(ci));
-            if (at != 0ull) {
-                const uint32_t F = (uint32_t)__ffsll((long long)at) - 1u;
-                if (tid == F) {
-                    s.bu[0] = bj;
-                    s.bd[0] = fx(ce);
-                }
-            } else if (tid == 0u) {  // unreachable by the argument above; never leave a stale answer
-                s.bu[0] = min(L * kPer + kPer - 1u, limit - 1u);
-                s.bd[0] = fx(base);
-            }
+    for (uint32_t j = 0; j < kPer; ++j) loc += (b0 + j < limit) ? h[b0 + j] : 0ull;
+    const unsigned long long incl = wave_incl_scan(loc, lane), run = incl - loc;
+    const unsigned long long hit = __ballot(loc != 0ull && fx(run) < target && target <= fx(incl));
+    if (hit == 0ull) {
+        *above = fx(lane_read(incl, 63));
+        return 0;
+    }
+    // the crossing lane's bins, bin j on lane j: exclusive sums from the lane's start
+    const uint32_t L = (uint32_t)__ffsll((long long)hit) - 1u;
+    const unsigned long long base = lane_read(run, (int)L);
+    const uint32_t bj = L * kPer + (lane & (kPer - 1u));
+    const unsigned long long hv = (lane < kPer && bj < limit) ? h[bj] : 0ull;
+    const unsigned long long ci = base + wave_incl_scan(hv, lane), ce = ci - hv;
+    // the first such bin exists: the sums are monotone and the lane's range holds target
+    const unsigned long long at = __ballot(hv != 0ull && fx(ce) < target && target <= fx(ci));
+    if (at == 0ull) {  // unreachable by the argument above; an answer inside the lane's range
+        *bin = min(L * kPer + kPer - 1u, limit - 1u);
+        *above = fx(base);
+        return 1;
+    }
+    const uint32_t F = (uint32_t)__ffsll((long long)at) - 1u;
+    *bin = L * kPer + F;
+    *above = fx(lane_read(ce, (int)F));
+    return 1;
+}
+
+// wave_cross for the whole block: wave 0 scans while the other waves wait at one barrier (a
+// block-wide scan costs several barriers, and each phase between them issues on four waves
+// per SIMD).
+__device__ inline int scan_cross(SelShared& s, const unsigned long long* h, uint32_t limit, double target,
+                                 uint32_t* bin, double* above) {
+    const uint32_t tid = threadIdx.x;
+    if (tid < 64u) {
+        uint32_t bn = 0xFFFFFFFFu;
+        double ab = 0.0;
+        if (!wave_cross(h, limit, target, &bn, &ab)) bn = 0xFFFFFFFFu;
+        if (tid == 0u) {
+            s.bu[0] = bn;
+            s.bd[0] = ab;
         }
     }
     __syncthreads();
@@ -534,35 +545,45 @@ __device__ __attribute__((always_inline)) inline void fv_hist(SelShared& s, cons
 
 // From complete histograms in s.vm / s.vq: the nucleus bin and the draw range.
 __device__ __attribute__((always_inline)) inline void fv_plan(SelShared& s, const RowCtx& c, float top_p, float u, FvPlan* P) {
-    const unsigned long long* hq = same_weights(c) ? s.vm : s.vq;
-    uint32_t bb;
-    // nucleus bin: where the T = 1 weight reaches top_p of the row total
-    uint32_t cb = kVBins;
-    double target_w = 0.0, wabove = 0.0, total = 0.0;
-    (void)scan_cross(s, s.vm, kVBins, INFINITY, &bb, &total);
-    P->total = total;
-    if (top_p < 1.0f) {
-        target_w = (double)top_p * total;
-        if (!scan_cross(s, s.vm, kVBins, target_w, &cb, &wabove)) cb = kVBins;
+    // wave 0 runs the five scans back to back and hands the plan over through LDS
+    FvPlan* sp = reinterpret_cast<FvPlan*>(s.cand);
+    if (threadIdx.x < 64u) {
+        const unsigned long long* hq = same_weights(c) ? s.vm : s.vq;
+        uint32_t bb;
+        // nucleus bin: where the T = 1 weight reaches top_p of the row total
+        uint32_t cb = kVBins;
+        double target_w = 0.0, wabove = 0.0, total = 0.0;
+        (void)wave_cross(s.vm, kVBins, INFINITY, &bb, &total);
+        if (top_p < 1.0f) {
+            target_w = (double)top_p * total;
+            if (!wave_cross(s.vm, kVBins, target_w, &cb, &wabove)) cb = kVBins;
+        }
+        // survivor weight bounds: A = bins above the nucleus bin, plus up to all of that bin
+        double A;
+        (void)wave_cross(hq, cb, INFINITY, &bb, &A);
+        const double Bq = (cb < kVBins) ? (double)hq[cb] / kFx : 0.0;
+        FvPlan q;
+        q.total = total;
+        q.cb = cb;
+        q.A = A;
+        q.target_w = target_w;
+        q.wabove = wabove;
+        q.u_zero = (u > 0.0f) ? 0u : 1u;
+        q.dlo = q.dhi = cb;
+        if (!q.u_zero) {
+            const uint32_t lim = (cb < kVBins) ? cb + 1u : kVBins;
+            uint32_t dlo = cb, dhi = cb;
+            double ab;
+            if (!wave_cross(hq, lim, (double)u * A, &dlo, &ab)) dlo = lim - 1u;
+            if (!wave_cross(hq, lim, (double)u * (A + Bq), &dhi, &ab)) dhi = lim - 1u;
+            q.dlo = dlo;
+            q.dhi = dhi;
+        }
+        if (threadIdx.x == 0u) *sp = q;
     }
-    // survivor weight bounds: A = bins above the nucleus bin, plus up to all of that bin
-    double A;
-    (void)scan_cross(s, hq, cb, INFINITY, &bb, &A);
-    const double Bq = (cb < kVBins) ? (double)hq[cb] / kFx : 0.0;
-    P->cb = cb;
-    P->A = A;
-    P->target_w = target_w;
-    P->wabove = wabove;
-    P->u_zero = (u > 0.0f) ? 0u : 1u;
-    P->dlo = P->dhi = cb;
-    if (P->u_zero) return;
-    const uint32_t lim = (cb < kVBins) ? cb + 1u : kVBins;
-    uint32_t dlo = cb, dhi = cb;
-    double ab;
-    if (!scan_cross(s, hq, lim, (double)u * A, &dlo, &ab)) dlo = lim - 1u;
-    if (!scan_cross(s, hq, lim, (double)u * (A + Bq), &dhi, &ab)) dhi = lim - 1u;
-    P->dlo = dlo;
-    P->dhi = dhi;
+    __syncthreads();
+    *P = *sp;
+    __syncthreads();
 }
 
 __device__ inline bool fv_wanted(const RowCtx& c, const FvPlan& P, float v) {
