@@ -568,6 +568,25 @@ def test_sampler_vocabulary_past_register_tiles(kind):
         h.close()
 
 
+def test_full_vocab_one_workgroup_path(head):
+    """Batches above 64 rows take the one-workgroup full-vocabulary path (histogram pass, plan,
+    gather pass, finish in one workgroup per row) instead of the multi-workgroup one. Half the
+    rows hold a first eighth far below the rest (below the value bins' range, so in the last
+    bin). Every row gives the oracle sampler's token."""
+    h, _ = head
+    Bn = 72
+    base = (synth.normal(7, 82, Bn * V).reshape(Bn, V) * 4).astype(np.float32)
+    base[1::2, : V // 8] -= 60.0
+    ts, ps = [1.0, 0.7, 1.3, 1.0], [0.9, 0.95, 0.5, 1.0]
+    rows = [T.row_default(temperature=ts[i % 4], top_p=ps[(i // 2) % 4], seed=40 + i, counter=3,
+                          flags=T.TURBO_ROW_FULL_VOCAB) for i in range(Bn)]
+    toks, after, rep = sample_given(h, base, rows)
+    assert np.array_equal(after, base)
+    check_sampler_on_gpu_logits(rows, toks, base, [T.row_uniform(r) for r in rows])
+    paths = rep.view(np.uint32)[:, 5]
+    assert np.all(paths == 2), paths
+
+
 def test_full_history_reports_and_fails_the_next_sync(head):
     """TURBO_STEP_APPEND_HISTORY on a row whose history already holds history_stride ids: the
     token is still produced, but not appended (history_len unchanged); the row's report carries
