@@ -488,6 +488,75 @@ __device__ inline int wave_cross(const unsigned long long* h, uint32_t limit, do
     return 1;
 }
 
+// One wave's lane sums of a kVBins histogram (lane l: bins 32 l .. 32 l + 31, exact integers)
+// and their inclusive and exclusive prefixes, for several crossing searches over one histogram.
+struct WaveHist {
+    unsigned long long loc, incl, run;
+};
+__device__ inline WaveHist wave_hist(const unsigned long long* h) {
+    constexpr uint32_t kPer = kVBins / 64u;
+    const uint32_t lane = threadIdx.x & 63u, b0 = lane * kPer;
+    WaveHist w;
+    w.loc = 0ull;
+#pragma unroll 8
+    for (uint32_t j = 0; j < kPer; ++j) w.loc += h[b0 + j];
+    w.incl = wave_incl_scan(w.loc, lane);
+    w.run = w.incl - w.loc;
+    return w;
+}
+
+// The bins of lane L (bin 32 L + j on lane j, bins at or past limit counted as 0) from base, the
+// weight below them: the first bin where the running total reaches target. Returns 1 with bin
+// and the weight before it, or 0 with *total = base + the lane's bins below limit.
+__device__ inline int lane_cross(const unsigned long long* h, uint32_t L, unsigned long long base, uint32_t limit,
+                                 double target, uint32_t* bin, double* before, double* total) {
+    constexpr uint32_t kPer = kVBins / 64u;
+    const uint32_t lane = threadIdx.x & 63u;
+    auto fx = [](unsigned long long v) { return (double)v / kFx; };
+    const uint32_t bj = L * kPer + (lane & (kPer - 1u));
+    const unsigned long long hv = (lane < kPer && bj < limit) ? h[bj] : 0ull;
+    const unsigned long long ci = base + wave_incl_scan(hv, lane), ce = ci - hv;
+    const unsigned long long at = __ballot(hv != 0ull && fx(ce) < target && target <= fx(ci));
+    if (at == 0ull) {
+        *total = fx(lane_read(ci, 63));
+        return 0;
+    }
+    const uint32_t F = (uint32_t)__ffsll((long long)at) - 1u;
+    *bin = L * kPer + F;
+    *before = fx(lane_read(ce, (int)F));
+    return 1;
+}
+
+// wave_cross over bins [0, limit) of h from its lane sums H (the same answers): lanes whose bins
+// all lie below limit are searched on H, and the lane holding limit, if any, bin by bin.
+__device__ inline int wave_cross_pre(const unsigned long long* h, const WaveHist& H, uint32_t limit, double target,
+                                     uint32_t* bin, double* above) {
+    constexpr uint32_t kPer = kVBins / 64u;
+    const uint32_t lane = threadIdx.x & 63u;
+    auto fx = [](unsigned long long v) { return (double)v / kFx; };
+    const uint32_t Lfull = limit / kPer;  // lanes 0 .. Lfull - 1 lie wholly below limit
+    const unsigned long long hit =
+        __ballot(lane < Lfull && H.loc != 0ull && fx(H.run) < target && target <= fx(H.incl));
+    if (hit != 0ull) {
+        const uint32_t L = (uint32_t)__ffsll((long long)hit) - 1u;
+        double tot;
+        if (lane_cross(h, L, lane_read(H.run, (int)L), limit, target, bin, above, &tot)) return 1;
+        // unreachable: the sums are monotone and lane L's range holds target
+        *bin = L * kPer + kPer - 1u;
+        *above = fx(lane_read(H.run, (int)L));
+        return 1;
+    }
+    const unsigned long long base = (Lfull > 0u) ? lane_read(H.incl, (int)Lfull - 1) : 0ull;
+    if (Lfull < 64u && Lfull * kPer < limit) {
+        double tot;
+        if (lane_cross(h, Lfull, base, limit, target, bin, above, &tot)) return 1;
+        *above = tot;
+        return 0;
+    }
+    *above = fx(base);
+    return 0;
+}
+
 // wave_cross for the whole block: wave 0 scans while the other waves wait at one barrier (a
 // block-wide scan costs several barriers, and each phase between them issues on four waves
 // per SIMD).
@@ -545,22 +614,26 @@ __device__ __attribute__((always_inline)) inline void fv_hist(SelShared& s, cons
 
 // From complete histograms in s.vm / s.vq: the nucleus bin and the draw range.
 __device__ __attribute__((always_inline)) inline void fv_plan(SelShared& s, const RowCtx& c, float top_p, float u, FvPlan* P) {
-    // wave 0 runs the five scans back to back and hands the plan over through LDS
+    // wave 0 runs the five scans back to back on lane sums taken once per histogram, and hands
+    // the plan over through LDS
     FvPlan* sp = reinterpret_cast<FvPlan*>(s.cand);
     if (threadIdx.x < 64u) {
-        const unsigned long long* hq = same_weights(c) ? s.vm : s.vq;
+        const bool same = same_weights(c);
+        const unsigned long long* hq = same ? s.vm : s.vq;
+        const WaveHist Hm = wave_hist(s.vm);
+        const WaveHist Hq = same ? Hm : wave_hist(s.vq);
         uint32_t bb;
         // nucleus bin: where the T = 1 weight reaches top_p of the row total
         uint32_t cb = kVBins;
         double target_w = 0.0, wabove = 0.0, total = 0.0;
-        (void)wave_cross(s.vm, kVBins, INFINITY, &bb, &total);
+        (void)wave_cross_pre(s.vm, Hm, kVBins, INFINITY, &bb, &total);
         if (top_p < 1.0f) {
             target_w = (double)top_p * total;
-            if (!wave_cross(s.vm, kVBins, target_w, &cb, &wabove)) cb = kVBins;
+            if (!wave_cross_pre(s.vm, Hm, kVBins, target_w, &cb, &wabove)) cb = kVBins;
         }
         // survivor weight bounds: A = bins above the nucleus bin, plus up to all of that bin
         double A;
-        (void)wave_cross(hq, cb, INFINITY, &bb, &A);
+        (void)wave_cross_pre(hq, Hq, cb, INFINITY, &bb, &A);
         const double Bq = (cb < kVBins) ? (double)hq[cb] / kFx : 0.0;
         FvPlan q;
         q.total = total;
@@ -574,8 +647,8 @@ __device__ __attribute__((always_inline)) inline void fv_plan(SelShared& s, cons
             const uint32_t lim = (cb < kVBins) ? cb + 1u : kVBins;
             uint32_t dlo = cb, dhi = cb;
             double ab;
-            if (!wave_cross(hq, lim, (double)u * A, &dlo, &ab)) dlo = lim - 1u;
-            if (!wave_cross(hq, lim, (double)u * (A + Bq), &dhi, &ab)) dhi = lim - 1u;
+            if (!wave_cross_pre(hq, Hq, lim, (double)u * A, &dlo, &ab)) dlo = lim - 1u;
+            if (!wave_cross_pre(hq, Hq, lim, (double)u * (A + Bq), &dhi, &ab)) dhi = lim - 1u;
             q.dlo = dlo;
             q.dhi = dhi;
         }
