@@ -447,47 +447,6 @@ __device__ __attribute__((always_inline)) inline int find_cross(SelShared& s, co
 
 // ---- full-vocabulary path on value bins ------------------------------------------------------------
 
-// Weight-histogram scan from bin 0 up over bins [0, limit) of h (kVBins u64 fixed-point
-// weights), by the 64 lanes of one wave: the bin where the running total first reaches target
-// (before < target <= before + h[bin]). Returns 1 with bin and the weight before it, or 0 with
-// the total when target exceeds it; every lane gets the same answer. Each lane adds 32 bins as
-// exact integers, a wave scan finds the lane whose range holds the crossing, and that lane's 32
-// bins, one per lane, find the bin.
-__device__ inline int wave_cross(const unsigned long long* h, uint32_t limit, double target, uint32_t* bin,
-                                 double* above) {
-    constexpr uint32_t kPer = kVBins / 64u;
-    static_assert(kPer <= 64u, "the crossing lane's bins are resolved one per lane");
-    const uint32_t lane = threadIdx.x & 63u;
-    auto fx = [](unsigned long long v) { return (double)v / kFx; };
-    const uint32_t b0 = lane * kPer;
-    unsigned long long loc = 0ull;
-#pragma unroll 8
-    for (uint32_t j = 0; j < kPer; ++j) loc += (b0 + j < limit) ? h[b0 + j] : 0ull;
-    const unsigned long long incl = wave_incl_scan(loc, lane), run = incl - loc;
-    const unsigned long long hit = __ballot(loc != 0ull && fx(run) < target && target <= fx(incl));
-    if (hit == 0ull) {
-        *above = fx(lane_read(incl, 63));
-        return 0;
-    }
-    // the crossing lane's bins, bin j on lane j: exclusive sums from the lane's start
-    const uint32_t L = (uint32_t)__ffsll((long long)hit) - 1u;
-    const unsigned long long base = lane_read(run, (int)L);
-    const uint32_t bj = L * kPer + (lane & (kPer - 1u));
-    const unsigned long long hv = (lane < kPer && bj < limit) ? h[bj] : 0ull;
-    const unsigned long long ci = base + wave_incl_scan(hv, lane), ce = ci - hv;
-    // the first such bin exists: the sums are monotone and the lane's range holds target
-    const unsigned long long at = __ballot(hv != 0ull && fx(ce) < target && target <= fx(ci));
-    if (at == 0ull) {  // unreachable by the argument above; an answer inside the lane's range
-        *bin = min(L * kPer + kPer - 1u, limit - 1u);
-        *above = fx(base);
-        return 1;
-    }
-    const uint32_t F = (uint32_t)__ffsll((long long)at) - 1u;
-    *bin = L * kPer + F;
-    *above = fx(lane_read(ce, (int)F));
-    return 1;
-}
-
 // One wave's lane sums of a kVBins histogram (lane l: bins 32 l .. 32 l + 31, exact integers)
 // and their inclusive and exclusive prefixes, for several crossing searches over one histogram.
 struct WaveHist {
@@ -511,6 +470,7 @@ __device__ inline WaveHist wave_hist(const unsigned long long* h) {
 __device__ inline int lane_cross(const unsigned long long* h, uint32_t L, unsigned long long base, uint32_t limit,
                                  double target, uint32_t* bin, double* before, double* total) {
     constexpr uint32_t kPer = kVBins / 64u;
+    static_assert(kPer <= 64u, "a lane's bins are resolved one per lane");
     const uint32_t lane = threadIdx.x & 63u;
     auto fx = [](unsigned long long v) { return (double)v / kFx; };
     const uint32_t bj = L * kPer + (lane & (kPer - 1u));
@@ -524,6 +484,37 @@ __device__ inline int lane_cross(const unsigned long long* h, uint32_t L, unsign
     const uint32_t F = (uint32_t)__ffsll((long long)at) - 1u;
     *bin = L * kPer + F;
     *before = fx(lane_read(ce, (int)F));
+    return 1;
+}
+
+// Weight-histogram scan from bin 0 up over bins [0, limit) of h (kVBins u64 fixed-point
+// weights), by the 64 lanes of one wave: the bin where the running total first reaches target
+// (before < target <= before + h[bin]). Returns 1 with bin and the weight before it, or 0 with
+// the total when target exceeds it; every lane gets the same answer. Each lane adds 32 bins as
+// exact integers, a wave scan finds the lane whose range holds the crossing, and that lane's 32
+// bins, one per lane, find the bin (lane_cross).
+__device__ inline int wave_cross(const unsigned long long* h, uint32_t limit, double target, uint32_t* bin,
+                                 double* above) {
+    constexpr uint32_t kPer = kVBins / 64u;
+    const uint32_t lane = threadIdx.x & 63u;
+    auto fx = [](unsigned long long v) { return (double)v / kFx; };
+    const uint32_t b0 = lane * kPer;
+    unsigned long long loc = 0ull;
+#pragma unroll 8
+    for (uint32_t j = 0; j < kPer; ++j) loc += (b0 + j < limit) ? h[b0 + j] : 0ull;
+    const unsigned long long incl = wave_incl_scan(loc, lane), run = incl - loc;
+    const unsigned long long hit = __ballot(loc != 0ull && fx(run) < target && target <= fx(incl));
+    if (hit == 0ull) {
+        *above = fx(lane_read(incl, 63));
+        return 0;
+    }
+    const uint32_t L = (uint32_t)__ffsll((long long)hit) - 1u;
+    const unsigned long long base = lane_read(run, (int)L);
+    double tot;
+    if (lane_cross(h, L, base, limit, target, bin, above, &tot)) return 1;
+    // unreachable: the sums are monotone and lane L's range holds target
+    *bin = min(L * kPer + kPer - 1u, limit - 1u);
+    *above = fx(base);
     return 1;
 }
 
