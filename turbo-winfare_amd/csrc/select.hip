@@ -452,7 +452,7 @@ __device__ __attribute__((always_inline)) inline int find_cross(SelShared& s, co
 struct WaveHist {
     unsigned long long loc, incl, run;
 };
-__device__ inline WaveHist wave_hist(const unsigned long long* h) {
+__device__ __attribute__((always_inline)) inline WaveHist wave_hist(const unsigned long long* h) {
     constexpr uint32_t kPer = kVBins / 64u;
     const uint32_t lane = threadIdx.x & 63u, b0 = lane * kPer;
     WaveHist w;
@@ -464,103 +464,92 @@ __device__ inline WaveHist wave_hist(const unsigned long long* h) {
     return w;
 }
 
+// A crossing search's answer, returned by value (out-parameters chosen per path kept these
+// values in scratch memory): found with the bin and the weight before it, or not found with
+// the weight of the whole range searched.
+struct Cross {
+    int found;
+    uint32_t bin;
+    double w;
+};
+
+__device__ inline double fx_of(unsigned long long v) { return (double)v / kFx; }
+
 // The bins of lane L (bin 32 L + j on lane j, bins at or past limit counted as 0) from base, the
-// weight below them: the first bin where the running total reaches target. Returns 1 with bin
-// and the weight before it, or 0 with *total = base + the lane's bins below limit.
-__device__ inline int lane_cross(const unsigned long long* h, uint32_t L, unsigned long long base, uint32_t limit,
-                                 double target, uint32_t* bin, double* before, double* total) {
+// weight below them: the first bin where the running total reaches target.
+__device__ __attribute__((always_inline)) inline Cross lane_cross(const unsigned long long* h, uint32_t L,
+                                                                  unsigned long long base, uint32_t limit,
+                                                                  double target) {
     constexpr uint32_t kPer = kVBins / 64u;
     static_assert(kPer <= 64u, "a lane's bins are resolved one per lane");
     const uint32_t lane = threadIdx.x & 63u;
-    auto fx = [](unsigned long long v) { return (double)v / kFx; };
     const uint32_t bj = L * kPer + (lane & (kPer - 1u));
     const unsigned long long hv = (lane < kPer && bj < limit) ? h[bj] : 0ull;
     const unsigned long long ci = base + wave_incl_scan(hv, lane), ce = ci - hv;
-    const unsigned long long at = __ballot(hv != 0ull && fx(ce) < target && target <= fx(ci));
-    if (at == 0ull) {
-        *total = fx(lane_read(ci, 63));
-        return 0;
-    }
+    const unsigned long long at = __ballot(hv != 0ull && fx_of(ce) < target && target <= fx_of(ci));
+    if (at == 0ull) return Cross{0, 0u, fx_of(lane_read(ci, 63))};
     const uint32_t F = (uint32_t)__ffsll((long long)at) - 1u;
-    *bin = L * kPer + F;
-    *before = fx(lane_read(ce, (int)F));
-    return 1;
+    return Cross{1, L * kPer + F, fx_of(lane_read(ce, (int)F))};
 }
 
 // Weight-histogram scan from bin 0 up over bins [0, limit) of h (kVBins u64 fixed-point
 // weights), by the 64 lanes of one wave: the bin where the running total first reaches target
-// (before < target <= before + h[bin]). Returns 1 with bin and the weight before it, or 0 with
-// the total when target exceeds it; every lane gets the same answer. Each lane adds 32 bins as
-// exact integers, a wave scan finds the lane whose range holds the crossing, and that lane's 32
-// bins, one per lane, find the bin (lane_cross).
-__device__ inline int wave_cross(const unsigned long long* h, uint32_t limit, double target, uint32_t* bin,
-                                 double* above) {
+// (before < target <= before + h[bin]), or not found with the total of the range; every lane
+// gets the same answer. Each lane adds 32 bins as exact integers, a wave scan finds the lane
+// whose range holds the crossing, and that lane's 32 bins, one per lane, find the bin.
+__device__ __attribute__((always_inline)) inline Cross wave_cross(const unsigned long long* h, uint32_t limit,
+                                                                  double target) {
     constexpr uint32_t kPer = kVBins / 64u;
     const uint32_t lane = threadIdx.x & 63u;
-    auto fx = [](unsigned long long v) { return (double)v / kFx; };
     const uint32_t b0 = lane * kPer;
     unsigned long long loc = 0ull;
 #pragma unroll 8
     for (uint32_t j = 0; j < kPer; ++j) loc += (b0 + j < limit) ? h[b0 + j] : 0ull;
     const unsigned long long incl = wave_incl_scan(loc, lane), run = incl - loc;
-    const unsigned long long hit = __ballot(loc != 0ull && fx(run) < target && target <= fx(incl));
-    if (hit == 0ull) {
-        *above = fx(lane_read(incl, 63));
-        return 0;
-    }
+    const unsigned long long hit = __ballot(loc != 0ull && fx_of(run) < target && target <= fx_of(incl));
+    if (hit == 0ull) return Cross{0, 0u, fx_of(lane_read(incl, 63))};
     const uint32_t L = (uint32_t)__ffsll((long long)hit) - 1u;
     const unsigned long long base = lane_read(run, (int)L);
-    double tot;
-    if (lane_cross(h, L, base, limit, target, bin, above, &tot)) return 1;
+    const Cross r = lane_cross(h, L, base, limit, target);
+    if (r.found) return r;
     // unreachable: the sums are monotone and lane L's range holds target
-    *bin = min(L * kPer + kPer - 1u, limit - 1u);
-    *above = fx(base);
-    return 1;
+    return Cross{1, min(L * kPer + kPer - 1u, limit - 1u), fx_of(base)};
 }
 
 // wave_cross over bins [0, limit) of h from its lane sums H (the same answers): lanes whose bins
 // all lie below limit are searched on H, and the lane holding limit, if any, bin by bin.
-__device__ inline int wave_cross_pre(const unsigned long long* h, const WaveHist& H, uint32_t limit, double target,
-                                     uint32_t* bin, double* above) {
+__device__ __attribute__((always_inline)) inline Cross wave_cross_pre(const unsigned long long* h, const WaveHist& H,
+                                                                      uint32_t limit, double target) {
     constexpr uint32_t kPer = kVBins / 64u;
     const uint32_t lane = threadIdx.x & 63u;
-    auto fx = [](unsigned long long v) { return (double)v / kFx; };
     const uint32_t Lfull = limit / kPer;  // lanes 0 .. Lfull - 1 lie wholly below limit
     const unsigned long long hit =
-        __ballot(lane < Lfull && H.loc != 0ull && fx(H.run) < target && target <= fx(H.incl));
+        __ballot(lane < Lfull && H.loc != 0ull && fx_of(H.run) < target && target <= fx_of(H.incl));
     if (hit != 0ull) {
         const uint32_t L = (uint32_t)__ffsll((long long)hit) - 1u;
-        double tot;
-        if (lane_cross(h, L, lane_read(H.run, (int)L), limit, target, bin, above, &tot)) return 1;
+        const unsigned long long base = lane_read(H.run, (int)L);
+        const Cross r = lane_cross(h, L, base, limit, target);
+        if (r.found) return r;
         // unreachable: the sums are monotone and lane L's range holds target
-        *bin = L * kPer + kPer - 1u;
-        *above = fx(lane_read(H.run, (int)L));
-        return 1;
+        return Cross{1, L * kPer + kPer - 1u, fx_of(base)};
     }
     const unsigned long long base = (Lfull > 0u) ? lane_read(H.incl, (int)Lfull - 1) : 0ull;
-    if (Lfull < 64u && Lfull * kPer < limit) {
-        double tot;
-        if (lane_cross(h, Lfull, base, limit, target, bin, above, &tot)) return 1;
-        *above = tot;
-        return 0;
-    }
-    *above = fx(base);
-    return 0;
+    if (Lfull < 64u && Lfull * kPer < limit) return lane_cross(h, Lfull, base, limit, target);
+    return Cross{0, 0u, fx_of(base)};
 }
 
 // wave_cross for the whole block: wave 0 scans while the other waves wait at one barrier (a
 // block-wide scan costs several barriers, and each phase between them issues on four waves
-// per SIMD).
-__device__ inline int scan_cross(SelShared& s, const unsigned long long* h, uint32_t limit, double target,
-                                 uint32_t* bin, double* above) {
+// per SIMD). Returns 1 with bin/above, or 0 with *above = the range's total.
+__device__ __attribute__((always_inline)) inline int scan_cross(SelShared& s, const unsigned long long* h,
+                                                                uint32_t limit, double target, uint32_t* bin,
+                                                                double* above) {
     const uint32_t tid = threadIdx.x;
     if (tid < 64u) {
-        uint32_t bn = 0xFFFFFFFFu;
-        double ab = 0.0;
-        if (!wave_cross(h, limit, target, &bn, &ab)) bn = 0xFFFFFFFFu;
+        const Cross r = wave_cross(h, limit, target);
         if (tid == 0u) {
-            s.bu[0] = bn;
-            s.bd[0] = ab;
+            s.bu[0] = r.found ? r.bin : 0xFFFFFFFFu;
+            s.bd[0] = r.w;
         }
     }
     __syncthreads();
@@ -613,18 +602,20 @@ __device__ __attribute__((always_inline)) inline void fv_plan(SelShared& s, cons
         const unsigned long long* hq = same ? s.vm : s.vq;
         const WaveHist Hm = wave_hist(s.vm);
         const WaveHist Hq = same ? Hm : wave_hist(s.vq);
-        uint32_t bb;
         // nucleus bin: where the T = 1 weight reaches top_p of the row total
         uint32_t cb = kVBins;
-        double target_w = 0.0, wabove = 0.0, total = 0.0;
-        (void)wave_cross_pre(s.vm, Hm, kVBins, INFINITY, &bb, &total);
+        double target_w = 0.0, wabove = 0.0;
+        const double total = wave_cross_pre(s.vm, Hm, kVBins, INFINITY).w;
         if (top_p < 1.0f) {
             target_w = (double)top_p * total;
-            if (!wave_cross_pre(s.vm, Hm, kVBins, target_w, &cb, &wabove)) cb = kVBins;
+            const Cross r = wave_cross_pre(s.vm, Hm, kVBins, target_w);
+            if (r.found) {
+                cb = r.bin;
+                wabove = r.w;
+            }
         }
         // survivor weight bounds: A = bins above the nucleus bin, plus up to all of that bin
-        double A;
-        (void)wave_cross_pre(hq, Hq, cb, INFINITY, &bb, &A);
+        const double A = wave_cross_pre(hq, Hq, cb, INFINITY).w;
         const double Bq = (cb < kVBins) ? (double)hq[cb] / kFx : 0.0;
         FvPlan q;
         q.total = total;
@@ -636,12 +627,10 @@ __device__ __attribute__((always_inline)) inline void fv_plan(SelShared& s, cons
         q.dlo = q.dhi = cb;
         if (!q.u_zero) {
             const uint32_t lim = (cb < kVBins) ? cb + 1u : kVBins;
-            uint32_t dlo = cb, dhi = cb;
-            double ab;
-            if (!wave_cross_pre(hq, Hq, lim, (double)u * A, &dlo, &ab)) dlo = lim - 1u;
-            if (!wave_cross_pre(hq, Hq, lim, (double)u * (A + Bq), &dhi, &ab)) dhi = lim - 1u;
-            q.dlo = dlo;
-            q.dhi = dhi;
+            const Cross lo = wave_cross_pre(hq, Hq, lim, (double)u * A);
+            const Cross hi = wave_cross_pre(hq, Hq, lim, (double)u * (A + Bq));
+            q.dlo = lo.found ? lo.bin : lim - 1u;
+            q.dhi = hi.found ? hi.bin : lim - 1u;
         }
         if (threadIdx.x == 0u) *sp = q;
     }
