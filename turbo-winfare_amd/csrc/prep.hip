@@ -266,6 +266,45 @@ __device__ void history_counts(const PrepArgs& a, uint32_t b, unsigned long long
     }
 }
 
+// Exclusive prefix sums of v[0, n) in place (LDS, every thread of the block calls it): each thread
+// adds a contiguous chunk, a wave scan and one pass over the wave totals place the chunks. Returns
+// the total; ends with a barrier.
+__device__ uint32_t block_excl_scan_lds(uint32_t* v, uint32_t n, uint32_t* s_scan, uint32_t* s_tot) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t per = (n + kPrepThreads - 1u) / kPrepThreads, i0 = tid * per;
+    uint32_t sum = 0u;
+    for (uint32_t i = i0; i < i0 + per && i < n; ++i) sum += v[i];
+    const uint32_t incl = wave_incl_scan(sum, lane);
+    if (lane == 63u) s_scan[wave] = incl;
+    __syncthreads();
+    if (tid == 0u) {
+        uint32_t run = 0u;
+        for (uint32_t w = 0; w < kPrepWaves; ++w) { const uint32_t t = s_scan[w]; s_scan[w] = run; run += t; }
+        *s_tot = run;
+    }
+    __syncthreads();
+    uint32_t run = s_scan[wave] + incl - sum;
+    for (uint32_t i = i0; i < i0 + per && i < n; ++i) {
+        const uint32_t c = v[i];
+        v[i] = run;
+        run += c;
+    }
+    const uint32_t tot = *s_tot;
+    __syncthreads();
+    return tot;
+}
+
+// LDS words of the tile-bucket bias table of a row (two counters per tile and one past the last,
+// then the keys and values of the list), or 0 when the counters alone would take more than 64 KB
+// (the sort path then builds the table).
+__host__ __device__ inline uint32_t bias_bucket_lds(uint32_t ntile, uint32_t P) {
+    const uint32_t counters = 2u * (ntile + 1u);
+    if (counters * 4u > 65536u) return 0u;
+    return ((counters + 1u) & ~1u) * 4u + P * 12u;
+}
+// A tile holding more list entries than this sorts the whole row instead.
+constexpr uint32_t kBucketMaxRun = 32;
+
 // part 0: row b's history counts; part 1: row b's bias table (independent outputs, so the two
 // run in separate blocks at the same time).
 __device__ void modtable_row(const PrepArgs& a, uint32_t b, unsigned long long* keys, uint32_t part) {
@@ -281,9 +320,81 @@ __device__ void modtable_row(const PrepArgs& a, uint32_t b, unsigned long long* 
     }
     if (!(use & 2u) || !a.bias_ids) return;
     const uint32_t P = a.P;
+    const uint32_t nb = min(a.bias_count[b], a.bias_stride);
+    const uint32_t ntile = a.ntile;
+    if (bias_bucket_lds(ntile, P) != 0u) {
+        // Tile buckets instead of a sort of the whole list: count the entries per 64-id tile,
+        // place them by the prefix of the counts, sort each tile's few entries by (id, list
+        // position) in one thread, then count the distinct ids per tile and place those. The
+        // table comes out the same as from the sort below; a tile with more than kBucketMaxRun
+        // entries sends the row there instead.
+        __shared__ uint32_t s_tot, s_long;
+        uint32_t* cstart = reinterpret_cast<uint32_t*>(keys);   // [ntile + 1] counts, then starts
+        uint32_t* fill = cstart + (ntile + 1u);                 // [ntile + 1] fill pointers, then distinct counts
+        unsigned long long* slot = keys + ((2u * (ntile + 1u) + 1u) >> 1);  // [P] keys by tile
+        float* vals = reinterpret_cast<float*>(slot + P);                    // [P] values by list position
+        const uint32_t* ids = a.bias_ids + (size_t)b * a.bias_stride;
+        for (uint32_t t = tid; t <= ntile; t += kPrepThreads) cstart[t] = 0u;
+        if (tid == 0u) s_long = 0u;
+        __syncthreads();
+        for (uint32_t i = tid; i < nb; i += kPrepThreads) {
+            const uint32_t id = ids[i];
+            vals[i] = a.bias_vals[(size_t)b * a.bias_stride + i];
+            if (id < V) atomicAdd(&cstart[id / kTileRows], 1u);
+        }
+        __syncthreads();
+        for (uint32_t t = tid; t < ntile; t += kPrepThreads)
+            if (cstart[t] > kBucketMaxRun) s_long = 1u;
+        __syncthreads();
+        if (s_long == 0u) {
+            (void)block_excl_scan_lds(cstart, ntile + 1u, s_scan, &s_tot);
+            for (uint32_t t = tid; t <= ntile; t += kPrepThreads) fill[t] = cstart[t];
+            __syncthreads();
+            for (uint32_t i = tid; i < nb; i += kPrepThreads) {
+                const uint32_t id = ids[i];
+                if (id < V) slot[atomicAdd(&fill[id / kTileRows], 1u)] = ((unsigned long long)id << 32) | i;
+            }
+            __syncthreads();
+            // each tile's entries ascending by (id, position), then its distinct ids counted
+            for (uint32_t t = tid; t < ntile; t += kPrepThreads) {
+                const uint32_t s0 = cstart[t], s1 = cstart[t + 1u];
+                for (uint32_t i = s0 + 1u; i < s1; ++i) {
+                    const unsigned long long k = slot[i];
+                    uint32_t j = i;
+                    while (j > s0 && slot[j - 1u] > k) { slot[j] = slot[j - 1u]; --j; }
+                    slot[j] = k;
+                }
+                uint32_t u = 0u;
+                for (uint32_t i = s0; i < s1; ++i) u += (i == s0 || (slot[i - 1u] >> 32) != (slot[i] >> 32)) ? 1u : 0u;
+                fill[t] = u;
+            }
+            if (tid == 0u) fill[ntile] = 0u;
+            __syncthreads();
+            const uint32_t nruns = block_excl_scan_lds(fill, ntile + 1u, s_scan, &s_tot);
+            // block_start[t] = entries with id < 64 t; one entry per id, its values summed in
+            // list order from 0.0f
+            uint32_t* bs = a.block_start + (size_t)b * (ntile + 1u);
+            ModEntry* mods = a.mods + (size_t)b * a.mod_cap;
+            for (uint32_t t = tid; t <= ntile; t += kPrepThreads) {
+                bs[t] = fill[t];
+                if (t == ntile) continue;
+                uint32_t e = fill[t];
+                const uint32_t s0 = cstart[t], s1 = cstart[t + 1u];
+                for (uint32_t i = s0; i < s1;) {
+                    const uint32_t id = (uint32_t)(slot[i] >> 32);
+                    float total = 0.0f;
+                    for (; i < s1 && (uint32_t)(slot[i] >> 32) == id; ++i) total = total + vals[(uint32_t)slot[i]];
+                    mods[e++] = ModEntry{id, 0u, total, 1u};
+                }
+            }
+            if (tid == 0u) a.mod_count[b] = nruns;
+            return;
+        }
+        // a long tile: the sort path below (its table layout differs; nothing of the above is kept)
+        __syncthreads();
+    }
     uint32_t* rs = reinterpret_cast<uint32_t*>(keys + P);  // run starts, [nruns + 1] <= P + 1
     float* vals = reinterpret_cast<float*>(rs + P + 2u);    // the list's values, by position
-    const uint32_t nb = min(a.bias_count[b], a.bias_stride);
     const unsigned long long kPad = ~0ull;
     for (uint32_t i = tid; i < P; i += kPrepThreads) {
         unsigned long long k = kPad;
@@ -335,7 +446,6 @@ __device__ void modtable_row(const PrepArgs& a, uint32_t b, unsigned long long* 
     // block_start[t] = number of entries with id < 64 t. Each thread covers a contiguous range of
     // tiles: one binary search over the run ids for its first tile, then a walk upwards (the ids
     // are sorted).
-    const uint32_t ntile = a.ntile;
     uint32_t* bs = a.block_start + (size_t)b * (ntile + 1u);
     const uint32_t tper = (ntile + 1u + kPrepThreads - 1u) / kPrepThreads;
     const uint32_t t0 = tid * tper;
@@ -398,7 +508,8 @@ void launch_step_prep(const Head& h, const PrepArgs& a, bool with_mods, hipStrea
         const size_t hist = 2u * kHistSlots * sizeof(uint32_t);
         const size_t bias = (size_t)a.P * sizeof(unsigned long long) + ((size_t)a.P + 2u) * sizeof(uint32_t) +
                             (size_t)a.P * sizeof(float);
-        lds = (std::max(hist, bias) + 15u) & ~(size_t)15u;
+        const size_t bucket = bias_bucket_lds(a.ntile, a.P);
+        lds = (std::max(std::max(hist, bias), bucket) + 15u) & ~(size_t)15u;
     }
     if (lds > 65536u) {
         static_assert(kModCap * 16u + 16u <= 160u * 1024u, "the largest table must fit one CU's LDS");
