@@ -135,10 +135,12 @@ bool launch_repack(const Head& h, const uint8_t* W, const uint16_t* S, const uin
 // History counts: the occurrences of each id < V (merged per id in LDS first) are added to
 // hcount[b][id] and the id's bit is set in hbits[b] (global atomics); the head epilogue zeroes
 // both as it reads them, so they are zero between steps.
-// Bias table: the bias entries are sorted by (id, list position) with a bitonic sort in LDS;
-// each run of equal ids becomes one entry whose value is the run's biases summed in list order
-// from 0.0f. Entries are written sorted by id; block_start[t] = number of entries with
-// id < 64 t comes from a binary search over the run ids.
+// Bias table: the bias entries in (id, list position) order, each run of equal ids becoming one
+// entry whose value is the run's biases summed in list order from 0.0f; entries are written
+// sorted by id, and block_start[t] = number of entries with id < 64 t. The order comes from
+// 64-id tile buckets (counts, their prefix, a small sort per tile) when the per-tile counters fit
+// the LDS and no tile holds more than kBucketMaxRun entries, else from a bitonic sort of the
+// whole list and a binary search over the run ids.
 constexpr uint32_t kPrepThreads = 1024;
 constexpr uint32_t kPrepWaves = kPrepThreads / 64;
 // LDS table merging a row's history occurrences per id: 2^kHistSlotBits slots of (id, count).
