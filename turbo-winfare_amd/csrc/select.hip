@@ -1,29 +1,37 @@
 // Token selection: greedy argmax or the sampled draw of sample_token (src/sampling.cpp:92-169).
 //
 // One 1024-thread workgroup per batch row, reading the row's final logits and the per-64-id
-// block partials the head epilogue wrote (max, lowest argmax, sum exp(l - max), finite min).
+// block partials the head epilogue wrote (max, lowest argmax, sum exp(l - max), finite min,
+// second-largest value).
 //
 //  greedy     argmax of the block partials, ties to the lowest id (:97-104).
 //  shortlist  (want = top_k, or 256 without the full-vocabulary flag; :122-137)
-//             tau = lower edge of the 22-bit key bin holding the want-th largest block maximum
-//             is a lower bound of the want-th largest logit, so every shortlist member lies in
-//             a block whose maximum is >= tau. Those blocks are gathered (elements >= tau),
-//             bitonic-sorted by (logit desc, id asc), and the first `want` form the shortlist.
-//             Nucleus over full-distribution probabilities (:139-151) and the temperature draw
-//             (:153-168) run as double-precision block scans over <= 256 candidates.
+//             tau, a lower bound of the want-th largest block maximum and so of the want-th
+//             largest logit: from a 256-bin window of width 1/32 below the row maximum, else a
+//             2048-bin histogram of the block maxima, else the exact 22-bit key bound. Every
+//             shortlist member lies in a block whose maximum is >= tau. A block whose
+//             second-largest value is below tau contributes only its maximum, taken from the
+//             partial; the other qualifying blocks are gathered (elements >= tau). The
+//             candidates are ranked by (logit desc, id asc) (counting ranks up to 256, a bitonic
+//             sort beyond), and the first `want` form the shortlist. Nucleus over
+//             full-distribution probabilities (:139-151) and the temperature draw (:153-168) run
+//             as double-precision scans (one wave up to 64 entries).
 //  full vocabulary (top_k = 0 with the full-vocabulary flag; the full-sort sampler of
 //             tests/test_sampling.cpp:36-84): one pass builds 2048-bin histograms of both the
 //             T = 1 and the temperature weights over equal-width logit-value bins spanning
-//             [lo, max] (bin order is rank order). The nucleus bin and the bins the draw can
-//             land in (bounded before the cut is known) are gathered in a second pass,
-//             bitonic-sorted, and resolved with double-precision scans.
+//             [lo, max] (bin order is rank order); one wave plans the nucleus bin and the bins
+//             the draw can land in (bounded before the cut is known), whose elements a second
+//             pass gathers. The crossings inside a bin are narrowed by 2048 sub-bins and resolved
+//             exactly over a sorted sub-bin. Batches up to 64 rows split each such row's passes
+//             over 16 workgroups (k_fv_hist, k_fv_gather, k_fv_finish).
 //  fallback   shortlist overflow or a bin too large to gather (massive ties): weighted radix
 //             select over the order-preserving keys, with ties among equal keys (equal
 //             weights) resolved by count and a radix select over ids.
 //
 // Weight histograms accumulate in LDS as u64 fixed point (w * 2^40, weights relative to the
 // row maximum are <= 1): integer LDS atomics run an order of magnitude faster than float ones
-// on gfx950. Truncation changes a row total by at most V * 2^-40 relative.
+// on gfx950. Truncation changes a row total by at most V * 2^-40 relative. Scans of those
+// histograms add exact integer sums.
 #include <stdexcept>
 
 #include "dt_internal.h"
@@ -31,10 +39,8 @@
 
 namespace tdt {
 
-// Workgroups run 1024 threads (bandwidth-bound full-vocabulary passes) or 256 (small batches,
-// where the per-row work is latency-bound: one wave per SIMD issues each uniform instruction
-// every 4 cycles instead of sharing the SIMD with three others). Device code reads the size at
-// run time.
+// Workgroups run 1024 threads. Device code reads the size at run time; a 512-thread form measured
+// slower on the B = 1 row, and the full-vocabulary passes want every wave for their loads.
 constexpr uint32_t kMaxSelThreads = 1024;
 constexpr uint32_t kMaxSelWaves = kMaxSelThreads / 64;
 __device__ inline uint32_t sel_nt() { return (uint32_t)__builtin_amdgcn_workgroup_size_x(); }
