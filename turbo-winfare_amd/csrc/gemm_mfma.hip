@@ -63,7 +63,9 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
     __shared__ __attribute__((aligned(16))) unsigned char pool[kLdsBytes];
     EpiMeta<NCOL>& meta = *reinterpret_cast<EpiMeta<NCOL>*>(pool + kPoolBytes);  // used only when META
 
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    // the wave index is uniform: in a scalar register, the DMA's LDS addresses (M0) and the tile
+    // offsets are scalar arithmetic, with no readfirstlane per DMA and no VGPRs holding them
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // Workgroup i is dispatched to XCD i % 8. The ncb column blocks of one group of four tiles go
     // to workgroups i, i + 8, ... of the same XCD, dispatched back to back, so every block after
     // the first finds the tiles' weights in that XCD's L2 instead of reading HBM again.
