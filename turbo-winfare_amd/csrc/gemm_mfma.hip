@@ -18,7 +18,8 @@
 //    (B = 256 runs two column blocks, on the same XCD back to back so the second reads the
 //    weights from L2). Weights and scales are prefetched PF groups ahead into registers by
 //    buffer loads; the activations reach a ring in LDS by buffer-to-LDS DMA, PF - 1 groups
-//    ahead, with one wait and one barrier per group.
+//    ahead, a group's DMA instructions spread over its k-steps, with one wait and one barrier
+//    per group.
 //  * Epilogue in place on the accumulators: per (column, 64-row tile), lane-local reductions
 //    and one cross-lane exchange give the block partial; logits leave as float4 stores.
 #include <hip/hip_ext.h>
@@ -103,13 +104,20 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
 #pragma unroll
         for (uint32_t i = 0; i < XDMA; ++i) buf_dma_16(xrs, pool + st * kStage + (4u * i + wave) * 1024u, xoff[i], g * 128u);
     };
-    // Every iteration issues, in this order, the DMA of a later group's activations, two scale
-    // loads and two weight loads. The DMA of group g + 1 is issued in iteration g + 2 - PF: when
-    // iteration g ends, its own iteration's four loads and PF - 2 whole iterations followed it, so
-    // waiting until at most that many are outstanding waits for it (with PF = 1 it was issued in
-    // iteration g itself). Where the DMA came from the prologue more followed it: the wait is
-    // stricter than needed there.
-    constexpr uint32_t kXWait = (PF > 1) ? 4u + (PF - 2u) * (XDMA + 4u) : 4u;
+    // In the main loop DMA instruction i of a later group's activations is issued at k-step i
+    // (0 at the top, beside the two scale loads), so the instructions do not hold up one k-step's
+    // MFMAs back to back; the two weight loads go at k-step 2. The DMA of group g + 1 is issued in
+    // iteration g + 2 - PF: when iteration g ends, the ops after its last instruction in that
+    // iteration (kAfter) and PF - 2 whole iterations followed it, so waiting until at most that
+    // many are outstanding waits for it (with PF = 1 it was issued in iteration g itself). Where
+    // the DMA came from the prologue (all of a group's instructions at once, before its loads)
+    // more followed it: the wait is stricter than needed there.
+    static_assert(XDMA == 1u || XDMA == 2u || XDMA == 4u, "a group's DMA instructions map onto its k-steps");
+    auto dma_one = [&](uint32_t g, uint32_t st, uint32_t i) {
+        buf_dma_16(xrs, pool + st * kStage + (4u * i + wave) * 1024u, xoff[i], g * 128u);
+    };
+    constexpr uint32_t kAfter = (XDMA == 1u) ? 4u : (XDMA == 2u) ? 2u : 0u;
+    constexpr uint32_t kXWait = (PF > 1) ? kAfter + (PF - 2u) * (XDMA + 4u) : kAfter;
     static_assert(kXWait < 64u, "vmcnt holds 6 bits");
 
     f16v acc[2][NB];
@@ -229,7 +237,7 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
             const uint32_t gx = min(g + (uint32_t)(PF > 1 ? PF - 1 : 1), G - 1u);
             const uint32_t gn = min(g + (uint32_t)PF, G - 1u);
             __builtin_amdgcn_sched_barrier(0);
-            dma_x(gx, stn);
+            dma_one(gx, stn, 0u);
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb) sbr[p][mb] = sload(gn, mb);
             __builtin_amdgcn_sched_barrier(0);
@@ -241,6 +249,11 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
             h8v bcur = bfrag(st, 0, 0);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
+                if (j >= 1 && (uint32_t)j < XDMA) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    dma_one(gx, stn, (uint32_t)j);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
 #pragma unroll
                 for (int mb = 0; mb < 2; ++mb) {
                     if (j < 3) {
