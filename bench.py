@@ -80,8 +80,8 @@ def head_kernel_name(B: int, meta: bool) -> str:
     if B <= 2:
         return f"k_head_digits_fused<{B}>"
     nb = 1 if B <= 32 else 2 if B <= 64 else 4
-    pf, occ = {1: (4, 3), 2: (2, 4), 4: (4, 2)}[nb]
-    return f"k_head_mfma<{nb}, {pf}, {occ}, true, {'true' if meta else 'false'}>"
+    wv, pf, occ = {1: (4, 4, 3), 2: (16, 2, 1), 4: (4, 4, 2)}[nb]
+    return f"k_head_mfma<{nb}, {wv}, {pf}, {occ}, true, {'true' if meta else 'false'}>"
 
 
 class Workload:

@@ -141,11 +141,11 @@ __device__ inline void softcap_values(float (&z)[N], const SoftcapPoly& p, float
 }
 
 // Modifier words of a workgroup's (tile, column) pairs, staged in LDS before the main loop:
-// w[t][c] = {history bitmap word 0, word 1, ban word 0, word 1, first bias entry, end}; and per
-// column r[c] = {has_mods, repetition, presence, frequency penalty bits}.
-template <uint32_t NCOL>
+// w[t][c] = {history bitmap word 0, word 1, ban word 0, word 1, first bias entry, end} for its
+// WV tiles; and per column r[c] = {has_mods, repetition, presence, frequency penalty bits}.
+template <int WV, uint32_t NCOL>
 struct EpiMeta {
-    uint32_t w[4][NCOL][6];
+    uint32_t w[WV][NCOL][6];
     uint32_t r[NCOL][4];
 };
 

@@ -14,9 +14,10 @@
 //    activation fragment is read from LDS with the same (chunk, word) mapping, and the
 //    activations are stored k-permuted within each octet as (x0, x4, x1, x5, x2, x6, x3, x7)
 //    to match the order the dequant produces halves in.
-//  * Workgroup = 4 waves, one 64-row tile each, over a block of 32*NB batch columns
+//  * Workgroup = WV waves, one 64-row tile each, over a block of 32*NB batch columns
 //    (B = 256 runs two column blocks, on the same XCD back to back so the second reads the
-//    weights from L2). Weights and scales are prefetched PF groups ahead into registers by
+//    weights from L2). At 64 columns one 16-wave workgroup per CU shares each activation stage
+//    among all 16 tiles; otherwise 4-wave workgroups run several to a CU. Weights and scales are prefetched PF groups ahead into registers by
 //    buffer loads; the activations reach a ring in LDS by buffer-to-LDS DMA, PF - 1 groups
 //    ahead, a group's DMA instructions spread over its k-steps, with one wait and one barrier
 //    per group.
@@ -32,9 +33,12 @@
 
 namespace tdt {
 
-// Workgroup = 4 waves, one 64-row tile each, over a block of NCOL = 32 NB batch columns
-// (the column block). Two or more independent workgroups share a CU, so one's epilogue overlaps
-// another's main loop and their barriers do not line up.
+// Workgroup = WV waves, one 64-row tile each, over a block of NCOL = 32 NB batch columns
+// (the column block). With WV = 4, two or more independent workgroups share a CU, so one's
+// epilogue overlaps another's main loop and their barriers do not line up. With WV = 16 (64
+// columns) the CU's one workgroup stages each group's activations once for its 16 tiles, a
+// quarter of the LDS fill and L2 reads of four 4-wave workgroups (B = 64 head 136 -> 125 us;
+// at 32 columns the same change measured 6 us slower, and 8 waves 2 - 5 us slower).
 // FULL: every column of the block exists (B % NCOL == 0): activation loads need no guard.
 // The main loop runs in rounds of PF groups (G % PF == 0) without branches: loads past the
 // last group are clamped to it and never used, so the compiler's load counters stay exact and
@@ -43,11 +47,11 @@ namespace tdt {
 // META: some row has modifiers or a ban mask; the workgroup's per-(tile, column) modifier words
 // are then staged in LDS before the main loop (their loads issue ahead of the weight stream), so
 // the epilogue reads them from LDS instead of waiting on global loads.
-template <int NB, int PF, int OCC, bool DENORM, bool META>
-__global__ __launch_bounds__(256, OCC) void k_head_mfma(
+template <int NB, int WV, int PF, int OCC, bool DENORM, bool META>
+__global__ __launch_bounds__(64 * WV, OCC) void k_head_mfma(
     const uint4* __restrict__ Wt, const uint32_t* __restrict__ SB16t,
     const uint16_t* __restrict__ x16, uint32_t B, uint32_t D, uint32_t NC, uint32_t G, uint32_t ncb, uint32_t ntg, EpiArgs ep) {
-    constexpr uint32_t NT = 256;
+    constexpr uint32_t NT = 64u * WV;
     constexpr uint32_t NCOL = 32 * NB;
     // Activations: group g (NCOL columns x 64 halves) lives in stage g % NST of a ring in LDS,
     // written by buffer-to-LDS DMA PF - 1 groups ahead (no registers, no LDS store instructions).
@@ -55,26 +59,29 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
     // fragment reads (16 lanes = 16 consecutive columns, one piece) then hit 64 distinct banks.
     constexpr uint32_t kStage = NCOL * 128u;
     constexpr uint32_t NST = PF > 1 ? PF : 2;
-    constexpr uint32_t XDMA = kStage / (NT * 16u);  // DMA instructions per thread per group
-    static_assert(kStage % (NT * 16u) == 0u, "a stage must split into whole 1 KiB DMA rows per wave");
+    // A stage is kRows 1 KiB rows, one DMA instruction each; row r is issued by wave r % WV
+    // (with fewer rows than waves, the first kRows waves issue one each and the rest none).
+    constexpr uint32_t kRows = kStage / 1024u;
+    constexpr uint32_t XDMA = (kRows + WV - 1u) / WV;  // DMA instructions per wave per group
+    static_assert(kStage % 1024u == 0u && (kRows % WV == 0u || kRows < WV), "a stage splits into whole DMA rows per wave");
     constexpr uint32_t kXBytes = NST * kStage;
-    constexpr uint32_t kTrBytes = 4u * kTrHalfFloats * 4u;  // the epilogue's four transposed half tiles
+    constexpr uint32_t kTrBytes = (uint32_t)WV * kTrHalfFloats * 4u;  // the epilogue's transposed half tiles, one per wave
     constexpr uint32_t kPoolBytes = kXBytes > kTrBytes ? kXBytes : kTrBytes;
-    constexpr uint32_t kLdsBytes = kPoolBytes + (META ? (uint32_t)sizeof(EpiMeta<NCOL>) : 0u);
+    constexpr uint32_t kLdsBytes = kPoolBytes + (META ? (uint32_t)sizeof(EpiMeta<WV, NCOL>) : 0u);
     __shared__ __attribute__((aligned(16))) unsigned char pool[kLdsBytes];
-    EpiMeta<NCOL>& meta = *reinterpret_cast<EpiMeta<NCOL>*>(pool + kPoolBytes);  // used only when META
+    EpiMeta<WV, NCOL>& meta = *reinterpret_cast<EpiMeta<WV, NCOL>*>(pool + kPoolBytes);  // used only when META
 
     // the wave index is uniform: in a scalar register, the DMA's LDS addresses (M0) and the tile
     // offsets are scalar arithmetic, with no readfirstlane per DMA and no VGPRs holding them
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    // Workgroup i is dispatched to XCD i % 8. The ncb column blocks of one group of four tiles go
+    // Workgroup i is dispatched to XCD i % 8. The ncb column blocks of one group of WV tiles go
     // to workgroups i, i + 8, ... of the same XCD, dispatched back to back, so every block after
     // the first finds the tiles' weights in that XCD's L2 instead of reading HBM again.
     const uint32_t wg = blockIdx.x, xcd = wg & 7u, slot = wg >> 3;
     const uint32_t tg = (slot / ncb) * 8u + xcd;
     if (tg >= ntg) return;                            // padding: ntg rounded up to 8
     const uint32_t cbase = (slot % ncb) * NCOL;       // first batch column of this workgroup
-    const uint32_t tile_raw = tg * 4u + wave;
+    const uint32_t tile_raw = tg * (uint32_t)WV + wave;
     const bool tile_ok = tile_raw < ep.ntile;
     const uint32_t tile = tile_ok ? tile_raw : ep.ntile - 1u;  // clamp loads; skip the epilogue
     const uint32_t hl = lane >> 5, l32 = lane & 31u;
@@ -91,18 +98,21 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
     auto sload = [&](uint32_t g, int mb) { return buf_load_b32(srs, soff + 128u * (uint32_t)mb, g * 256u); };
     const uint32_t magic = DENORM ? 0u : magic_vgpr();
 
-    // The DMA sources of this thread's pieces: instruction i of wave w fills slots
-    // (4 i + w) * 64 + lane of a stage. Columns past the batch read past the buffer's end (zeros).
+    // The DMA sources of this thread's pieces: instruction i of wave w fills row WV i + w, slots
+    // (WV i + w) * 64 + lane of a stage. Columns past the batch read past the buffer's end (zeros).
+    auto dma_row = [&](uint32_t i) { return (uint32_t)WV * i + wave; };
+    auto dma_on = [&](uint32_t i) { return kRows % WV == 0u || dma_row(i) < kRows; };  // uniform
     const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x16), 0, B * D * 2u, kBufDword3);
     uint32_t xoff[XDMA];
 #pragma unroll
     for (uint32_t i = 0; i < XDMA; ++i) {
-        const uint32_t sl = (4u * i + wave) * 64u + lane, c = sl >> 3, pc = (sl & 7u) ^ ((c >> 1) & 7u);
-        xoff[i] = (cbase + c < B) ? ((cbase + c) * D + 8u * pc) * 2u : B * D * 2u;
+        const uint32_t sl = dma_row(i) * 64u + lane, c = sl >> 3, pc = (sl & 7u) ^ ((c >> 1) & 7u);
+        xoff[i] = (dma_on(i) && cbase + c < B) ? ((cbase + c) * D + 8u * pc) * 2u : B * D * 2u;
     }
     auto dma_x = [&](uint32_t g, uint32_t st) {
 #pragma unroll
-        for (uint32_t i = 0; i < XDMA; ++i) buf_dma_16(xrs, pool + st * kStage + (4u * i + wave) * 1024u, xoff[i], g * 128u);
+        for (uint32_t i = 0; i < XDMA; ++i)
+            if (dma_on(i)) buf_dma_16(xrs, pool + st * kStage + dma_row(i) * 1024u, xoff[i], g * 128u);
     };
     // In the main loop DMA instruction i of a later group's activations is issued at k-step i
     // (0 at the top, beside the two scale loads), so the instructions do not hold up one k-step's
@@ -111,10 +121,11 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
     // iteration (kAfter) and PF - 2 whole iterations followed it, so waiting until at most that
     // many are outstanding waits for it (with PF = 1 it was issued in iteration g itself). Where
     // the DMA came from the prologue (all of a group's instructions at once, before its loads)
-    // more followed it: the wait is stricter than needed there.
+    // more followed it: the wait is stricter than needed there. A wave that issues no DMA waits
+    // for the same count over its own loads, which it needs by then anyway.
     static_assert(XDMA == 1u || XDMA == 2u || XDMA == 4u, "a group's DMA instructions map onto its k-steps");
     auto dma_one = [&](uint32_t g, uint32_t st, uint32_t i) {
-        buf_dma_16(xrs, pool + st * kStage + (4u * i + wave) * 1024u, xoff[i], g * 128u);
+        if (dma_on(i)) buf_dma_16(xrs, pool + st * kStage + dma_row(i) * 1024u, xoff[i], g * 128u);
     };
     constexpr uint32_t kAfter = (XDMA == 1u) ? 4u : (XDMA == 2u) ? 2u : 0u;
     constexpr uint32_t kXWait = (PF > 1) ? kAfter + (PF - 2u) * (XDMA + 4u) : kAfter;
@@ -130,18 +141,18 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
 
     // The modifier words of the workgroup's (tile, column) pairs, loaded before the weight
     // stream; they are stored to LDS after the prologue's wait, which covers them.
-    constexpr uint32_t kMetaPer = (4u * NCOL + NT - 1u) / NT;
+    constexpr uint32_t kMetaPer = ((uint32_t)WV * NCOL + NT - 1u) / NT;
     uint32_t mw[META ? kMetaPer : 1][6];
     uint32_t mr[META ? kMetaPer : 1][4];
     if constexpr (META) {
 #pragma unroll
         for (uint32_t q = 0; q < kMetaPer; ++q) {
-            const uint32_t idx = tid + q * NT, t = idx / NCOL, c = cbase + idx % NCOL, tl = tg * 4u + t;
+            const uint32_t idx = tid + q * NT, t = idx / NCOL, c = cbase + idx % NCOL, tl = tg * (uint32_t)WV + t;
 #pragma unroll
             for (int k = 0; k < 6; ++k) mw[q][k] = 0u;
 #pragma unroll
             for (int k = 0; k < 4; ++k) mr[q][k] = 0u;
-            if (idx < 4u * NCOL && c < B && tl < ep.ntile) {
+            if (idx < (uint32_t)WV * NCOL && c < B && tl < ep.ntile) {
                 const uint32_t* rw = reinterpret_cast<const uint32_t*>(ep.rows + c);
                 mr[q][0] = rw[9];  // has_mods
                 mr[q][1] = rw[3];  // repetition_penalty
@@ -187,7 +198,7 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
 #pragma unroll
         for (uint32_t q = 0; q < kMetaPer; ++q) {
             const uint32_t idx = tid + q * NT;
-            if (idx < 4u * NCOL) {
+            if (idx < (uint32_t)WV * NCOL) {
                 const uint32_t t = idx / NCOL, cl = idx % NCOL;
 #pragma unroll
                 for (int k = 0; k < 6; ++k) meta.w[t][cl][k] = mw[q][k];
@@ -220,12 +231,12 @@ __global__ __launch_bounds__(256, OCC) void k_head_mfma(
 #pragma unroll
         for (int p = 0; p < PF; ++p) {
             const uint32_t g = g0 + p;
-            // Up to 64 columns every workgroup is resident from the start (four per CU): even
-            // progress keeps all four streaming until the end (B = 32 head 94 -> 89 us, B = 64
-            // 141 -> 135 us). With four column blocks the workgroups come in rounds, and the
-            // staggered ends that age order gives overlap one round's epilogues with the next
-            // round's loop (there the priorities measured 12 us slower).
-            if constexpr (NB <= 2) prio_by_progress(g, G);
+            // At 32 columns every workgroup is resident from the start (four per CU): even
+            // progress keeps all four streaming until the end (B = 32 head 94 -> 89 us). With
+            // four column blocks the workgroups come in rounds, and the staggered ends that age
+            // order gives overlap one round's epilogues with the next round's loop (there the
+            // priorities measured 12 us slower). A 16-wave workgroup is alone on its CU.
+            if constexpr (NB <= 2 && WV == 4) prio_by_progress(g, G);
             // stage of group g; group g + PF - 1 goes to the stage group g - 1 used (every wave
             // finished with it before the last barrier)
             const uint32_t st = (PF > 1) ? (uint32_t)p : (g & 1u);
@@ -499,39 +510,39 @@ void launch_head_mfma(const Head& h, int batch, const EpiArgs& ep, hipStream_t s
     if (B > 256u) throw std::runtime_error("MFMA head supports batch <= 256");
     const int nb = (B <= 32u) ? 1 : (B <= 64u) ? 2 : 4;
     const uint32_t ncol = 32u * (uint32_t)nb;
-    const uint32_t ntg = (h.ntile + 3u) / 4u, ncb = (B + ncol - 1u) / ncol;
+    const uint32_t wv = (nb == 2) ? 16u : 4u;  // waves (tiles) per workgroup, as instantiated below
+    const uint32_t ntg = (h.ntile + wv - 1u) / wv, ncb = (B + ncol - 1u) / ncol;
     const dim3 grid(ncb * ((ntg + 7u) / 8u) * 8u);
     const bool meta = ep.meta != 0u;
     // Prefetch depth: four groups when the group count allows it, else two, else one. Two column
-    // blocks run at four workgroups per CU (all 1024 of a 262,144-row head resident at once, where
-    // three per CU left a second round of 256 running alone) and hold two groups, which fits the
-    // 128 registers that occupancy allows.
+    // blocks run as one 16-wave workgroup per CU (all 256 of a 262,144-row head resident at once)
+    // and hold two groups, which fits the 128 registers that sixteen waves per CU allow.
     const int pf = (h.G % 4u == 0u) ? 4 : (h.G % 2u == 0u) ? 2 : 1;
-#define TDT_LAUNCH(NB, PF, OCC, DN, MT)                                                                  \
-    hipExtLaunchKernelGGL((k_head_mfma<NB, PF, OCC, DN, MT>), grid, dim3(256), 0, st, ev0, ev1, 0, h.Wt, \
+#define TDT_LAUNCH(NB, WV, PF, OCC, DN, MT)                                                                   \
+    hipExtLaunchKernelGGL((k_head_mfma<NB, WV, PF, OCC, DN, MT>), grid, dim3(64 * WV), 0, st, ev0, ev1, 0, h.Wt, \
                           h.SB16t, h.x16, B, h.D, h.NC, h.G, ncb, ntg, ep)
-#define TDT_PF421(NB, OCC, DN, MT)                                 \
+#define TDT_PF421(NB, WV, OCC, DN, MT)                             \
     do {                                                           \
-        if (pf == 4) TDT_LAUNCH(NB, 4, OCC, DN, MT);                \
-        else if (pf == 2) TDT_LAUNCH(NB, 2, OCC, DN, MT);           \
-        else TDT_LAUNCH(NB, 1, OCC, DN, MT);                        \
+        if (pf == 4) TDT_LAUNCH(NB, WV, 4, OCC, DN, MT);            \
+        else if (pf == 2) TDT_LAUNCH(NB, WV, 2, OCC, DN, MT);       \
+        else TDT_LAUNCH(NB, WV, 1, OCC, DN, MT);                    \
     } while (0)
-#define TDT_PF21(NB, OCC, DN, MT)                                  \
+#define TDT_PF21(NB, WV, OCC, DN, MT)                              \
     do {                                                           \
-        if (pf >= 2) TDT_LAUNCH(NB, 2, OCC, DN, MT);                \
-        else TDT_LAUNCH(NB, 1, OCC, DN, MT);                        \
+        if (pf >= 2) TDT_LAUNCH(NB, WV, 2, OCC, DN, MT);            \
+        else TDT_LAUNCH(NB, WV, 1, OCC, DN, MT);                    \
     } while (0)
-#define TDT_PICK(NB, OCC, PFS)                                                            \
-    do {                                                                                  \
-        if (h.mfma_denorm) { if (meta) PFS(NB, OCC, true, true); else PFS(NB, OCC, true, false); } \
-        else { if (meta) PFS(NB, OCC, false, true); else PFS(NB, OCC, false, false); }             \
+#define TDT_PICK(NB, WV, OCC, PFS)                                                                         \
+    do {                                                                                                   \
+        if (h.mfma_denorm) { if (meta) PFS(NB, WV, OCC, true, true); else PFS(NB, WV, OCC, true, false); } \
+        else { if (meta) PFS(NB, WV, OCC, false, true); else PFS(NB, WV, OCC, false, false); }             \
     } while (0)
     if (nb == 1) {
-        TDT_PICK(1, 3, TDT_PF421);
+        TDT_PICK(1, 4, 3, TDT_PF421);
     } else if (nb == 2) {
-        TDT_PICK(2, 4, TDT_PF21);
+        TDT_PICK(2, 16, 1, TDT_PF21);
     } else {
-        TDT_PICK(4, 2, TDT_PF421);
+        TDT_PICK(4, 4, 2, TDT_PF421);
     }
 #undef TDT_PICK
 #undef TDT_PF21
