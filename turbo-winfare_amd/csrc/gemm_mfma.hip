@@ -39,7 +39,7 @@ namespace tdt {
 // columns) the CU's one workgroup stages each group's activations once for its 16 tiles, a
 // quarter of the LDS fill and L2 reads of four 4-wave workgroups (B = 64 head 136 -> 125 us;
 // at 32 columns the same change measured 6 us slower, and 8 waves 2 - 5 us slower).
-// FULL: every column of the block exists (B % NCOL == 0): activation loads need no guard.
+// Columns past the batch read zeros (their DMA source lies past the buffer's end).
 // The main loop runs in rounds of PF groups (G % PF == 0) without branches: loads past the
 // last group are clamped to it and never used, so the compiler's load counters stay exact and
 // the weight prefetch is never drained early. The next k-step's weights are dequantised in
