@@ -77,6 +77,27 @@ def test_logits_mfma_path(small_head, batch):
         assert e <= U.LOGIT_RTOL, (b, e)
 
 
+@pytest.mark.parametrize("vocab,batch", [(300, 40), (4099, 48), (1100, 33)])
+def test_logits_mfma_partial_workgroups(vocab, batch):
+    """64-column heads run 16 tiles per workgroup: vocabularies of 5, 65 and 18 tiles leave the
+    only or the last workgroup partly past the table, and batches of 33 - 48 rows a partial
+    column block (columns past the batch read zeros and store nothing)."""
+    W, S, B, g = synth.make_head(vocab, D, 105)
+    h = T.LMHead(W, S, B, g, vocab=vocab, hidden=D)
+    try:
+        x = np.stack([O.rms_norm(r, g, 1e-6) for r in synth.hidden_states(batch, D, 11)])
+        out = torch.full((batch + 1, vocab), 7.0, dtype=torch.float32, device="cuda")
+        h.logits(dev(x), batch, out)
+        h.sync()
+        got = out.cpu().numpy()
+        for b in sorted({0, 31, 32, batch - 1}):
+            want = O.softcap(O.matvec(W, S, B, x[b], U.THREADS), 30.0)
+            assert U.logit_err(got[b], want) <= U.LOGIT_RTOL, b
+        assert np.all(got[batch] == 7.0)  # the row past the batch is untouched
+    finally:
+        h.close()
+
+
 def test_logits_mfma_bf16_input(small_head):
     h, (W, S, B, g) = small_head
     xb = synth.f32_to_bf16(synth.hidden_states(8, D, 8))
