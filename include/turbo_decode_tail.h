@@ -31,6 +31,29 @@ extern "C" {
 
 #define TURBO_DT_API __attribute__((visibility("default")))
 
+/* ---- ABI version ------------------------------------------------------------------------- */
+
+/*
+ * No counterpart in the reference (its C API has one struct, checked by turbo_options_default).
+ * TURBO_DT_ABI_VERSION changes whenever a struct layout or an entry point's meaning changes.
+ * A caller compiled against this header checks, once at load time, that
+ * turbo_abi_version() == TURBO_DT_ABI_VERSION and that turbo_abi_struct_size() agrees with its
+ * sizeof for every struct it passes; a library of another layout would otherwise read or write
+ * past the caller's arrays (TurboRowReport per row, for example) without any error.
+ */
+#define TURBO_DT_ABI_VERSION 1u
+enum {
+    TURBO_ABI_LMHEAD_DESC = 0,    /* TurboLMHeadDesc */
+    TURBO_ABI_BUNDLE_TENSOR = 1,  /* TurboBundleTensor */
+    TURBO_ABI_SAMPLING_ROW = 2,   /* TurboSamplingRow */
+    TURBO_ABI_STEP_INPUTS = 3,    /* TurboStepInputs */
+    TURBO_ABI_ROW_REPORT = 4,     /* TurboRowReport */
+    TURBO_ABI_STEP_OUTPUTS = 5    /* TurboStepOutputs */
+};
+TURBO_DT_API uint32_t turbo_abi_version(void);
+/* sizeof of the struct TURBO_ABI_* names, as the library was built; 0 for an unknown id. */
+TURBO_DT_API size_t turbo_abi_struct_size(int which);
+
 /* ---- errors ------------------------------------------------------------------------------ */
 
 /* Replaces turbo_engine_last_error (include/gturbo/c_api.h:74-78; src/c_api.cpp:29-40). */
@@ -106,10 +129,14 @@ TURBO_DT_API void turbo_lmhead_desc_default(TurboLMHeadDesc* out);
  * Copies the table into HBM in the kernels' tiled layout (the caller's buffers may be freed
  * afterwards) and allocates per-step scratch. Replaces the resident upload and buffer set-up
  * of ForwardRunner::initialize for this path (src/runner.cpp:211-215, :260-292).
- * Returns NULL on failure.
+ * Returns NULL on failure. Batches above two rows compute on the matrix cores in fp16: a table
+ * with a scale or bias of magnitude above 65504 is accepted, but such calls on it then fail with
+ * an error (one- and two-row calls are unaffected). Hidden states have no such limit.
  */
 TURBO_DT_API void* turbo_lmhead_create(const TurboLMHeadDesc* desc);
-/* Drains the stream and frees everything (src/runner.cpp:25-42). NULL is a no-op. */
+/* Waits for the handle's stream (the one set by turbo_lmhead_set_stream, which must still exist;
+ * other streams are not waited for) and frees everything (src/runner.cpp:25-42). NULL is a
+ * no-op. */
 TURBO_DT_API void turbo_lmhead_destroy(void* handle);
 /* hip_stream is a hipStream_t (NULL = the null stream). Must be created at default priority. */
 TURBO_DT_API int turbo_lmhead_set_stream(void* handle, void* hip_stream);
@@ -269,6 +296,9 @@ TURBO_DT_API void* turbo_int4_matrix_create(uint32_t rows, uint32_t in_dim, int 
  * 0: host memory, staged through temporary device buffers and finished before the call returns. */
 TURBO_DT_API int turbo_int4_matrix_load(void* matrix, const uint8_t* weight, const uint16_t* scales,
                                         const uint16_t* biases, int weights_on_device, void* hip_stream);
+/* Waits for the streams the matrix's loads and products were enqueued on (the whole device when
+ * more than four distinct streams were used) and frees it. Calls that use one matrix handle are
+ * serialised by the caller. */
 TURBO_DT_API void turbo_int4_matrix_destroy(void* matrix);
 /* out[i][r] = sum_c (q[r][c] * scale + bias) * x[i][c] for each of `count` (0..32) matrices of one
  * device, in one kernel launch on hip_stream: for example the 8 routed experts' gate and up

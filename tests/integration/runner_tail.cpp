@@ -65,6 +65,14 @@ class DecodeTailRunner {
     // the bundle's resident index; per-request buffers sized for the longest generation.
     void initialize(const std::string& resident_path, float final_logit_softcap, float rms_norm_eps,
                     const float* z_host, uint32_t positions, uint32_t history_cap) {
+        // the library must have the layout this file was compiled against
+        if (turbo_abi_version() != TURBO_DT_ABI_VERSION ||
+            turbo_abi_struct_size(TURBO_ABI_SAMPLING_ROW) != sizeof(TurboSamplingRow) ||
+            turbo_abi_struct_size(TURBO_ABI_STEP_INPUTS) != sizeof(TurboStepInputs) ||
+            turbo_abi_struct_size(TURBO_ABI_STEP_OUTPUTS) != sizeof(TurboStepOutputs) ||
+            turbo_abi_struct_size(TURBO_ABI_ROW_REPORT) != sizeof(TurboRowReport) ||
+            turbo_abi_struct_size(TURBO_ABI_BUNDLE_TENSOR) != sizeof(TurboBundleTensor))
+            throw GTurboFormatError("libturbo_decode_tail.so has another ABI than turbo_decode_tail.h");
         hip_check(hipStreamCreate(&stream_), "hipStreamCreate");  // default priority
         lmhead_ = turbo_lmhead_create_from_bundle(resident_path.c_str(), final_logit_softcap, rms_norm_eps,
                                                   /*device=*/0);

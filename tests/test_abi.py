@@ -34,6 +34,18 @@ def test_struct_layouts():
     assert C.sizeof(T.TurboStepOutputs) == 24
 
 
+def test_abi_version_and_struct_sizes():
+    """The library reports the header's ABI version and, per struct, the size it was built with;
+    the ctypes mirror's layouts must agree with both."""
+    lib = T.load()
+    ver = int(re.search(r"#define TURBO_DT_ABI_VERSION (\d+)u", HEADER.read_text()).group(1))
+    assert lib.turbo_abi_version() == ver
+    for which, st in enumerate((T.TurboLMHeadDesc, T.TurboBundleTensor, T.TurboSamplingRow, T.TurboStepInputs,
+                                T.TurboRowReport, T.TurboStepOutputs)):
+        assert lib.turbo_abi_struct_size(which) == C.sizeof(st), st.__name__
+    assert lib.turbo_abi_struct_size(99) == 0
+
+
 def test_splitmix_and_seed_for():
     lib = T.load()
     assert lib.turbo_splitmix64(0) == 0xE220A8397B1DCDAF

@@ -77,6 +77,67 @@ def test_logits_mfma_path(small_head, batch):
         assert e <= U.LOGIT_RTOL, (b, e)
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("batch", [3, 64, 256])
+def test_logits_mfma_large_activations(small_head, batch, dtype):
+    """Normalised rows scaled far past the normalised range (largest |x| 1e4 and 6e4; at 6e4 even
+    the unscaled fp16 value is within 10 % of the fp16 maximum and 16 x would be infinite): the
+    step prep stores such a row times a power of two and the epilogue multiplies its accumulators
+    back, so its logits stay finite and within the tolerance of the oracle's fp32 ones. Rows
+    within range are bit-identical to the same rows in a batch without the large ones."""
+    h, (W, S, B, g) = small_head
+    base = np.stack([O.rms_norm(r, g, 1e-6) for r in synth.hidden_states(batch, D, 12)])
+    big = {0: 1.0e4, batch - 1: 6.0e4}
+    if batch >= 64:
+        big[batch // 2] = 2.5e3  # just past the 2^11 limit
+    x = base.copy()
+    for b, top in big.items():
+        x[b] = (base[b] * (top / np.abs(base[b]).max())).astype(np.float32)
+
+    def run(rows):
+        if dtype == "bf16":
+            xin, hd = synth.f32_to_bf16(rows), T.TURBO_HIDDEN_BF16
+        else:
+            xin, hd = rows, T.TURBO_HIDDEN_F32
+        out = torch.empty((batch, V_SMALL), dtype=torch.float32, device="cuda")
+        h.logits(dev(xin.view(np.int16) if dtype == "bf16" else xin), batch, out, dtype=hd, softcap=False)
+        h.sync()
+        return out.cpu().numpy()
+
+    got, ref = run(x), run(base)
+    for b, top in big.items():
+        xb = synth.bf16_to_f32(synth.f32_to_bf16(x[b])) if dtype == "bf16" else x[b]
+        want = O.matvec(W, S, B, xb, U.THREADS)
+        assert np.all(np.isfinite(got[b])), (b, int((~np.isfinite(got[b])).sum()))
+        e = U.logit_err(got[b], want)
+        assert e <= U.LOGIT_RTOL, (b, top, e)
+    keep = [b for b in range(batch) if b not in big]
+    assert np.array_equal(got[keep].view(np.uint32), ref[keep].view(np.uint32))
+
+
+def test_step_normed_large_activations(small_head):
+    """The same through turbo_lmhead_step with TURBO_STEP_NORMED (the caller's rows are not
+    normalised again): softcapped logits of rows reaching |x| = 3e4 against the oracle, and greedy
+    tokens that are the oracle's (or inside the stated near-tie margin)."""
+    h, (W, S, B, g) = small_head
+    Bn = 4
+    x = np.stack([O.rms_norm(r, g, 1e-6) for r in synth.hidden_states(Bn, D, 13)])
+    x[1] *= 3.0e4 / np.abs(x[1]).max()
+    x[3] *= 5.0e3 / np.abs(x[3]).max()
+    x = x.astype(np.float32)
+    rows = [T.row_default() for _ in range(Bn)]
+    inp, keep = h.make_inputs(Bn, rows, hidden=dev(x), flags=T.TURBO_STEP_NORMED)
+    tok = torch.zeros(Bn, dtype=torch.int32, device="cuda")
+    lg = torch.empty((Bn, V_SMALL), dtype=torch.float32, device="cuda")
+    h.step(inp, tok, lg)
+    h.sync()
+    got, toks = lg.cpu().numpy(), tok.cpu().numpy()
+    for b in range(Bn):
+        want = O.softcap(O.matvec(W, S, B, x[b], U.THREADS), 30.0)
+        assert U.logit_err(got[b], want) <= U.LOGIT_RTOL, b
+        assert U.draw_check(want, O.params(0.0), 0.0, int(toks[b]), mode="margin") in ("exact", "within")
+
+
 @pytest.mark.parametrize("vocab,batch", [(300, 40), (4099, 48), (1100, 33)])
 def test_logits_mfma_partial_workgroups(vocab, batch):
     """64-column heads run 16 tiles per workgroup: vocabularies of 5, 65 and 18 tiles leave the

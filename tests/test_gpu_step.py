@@ -8,6 +8,11 @@ Per configuration:
     (exact unless near a tie), which checks the selection independently of GEMV rounding;
   * modifiers are checked bit-exactly: the oracle applies them to the GPU's raw logits.
 Near-tie rows (margin < 1e-3 relative) are counted and printed, never silently dropped."""
+import hashlib
+import json
+import os
+from pathlib import Path
+
 import numpy as np
 import pytest
 
@@ -50,17 +55,21 @@ def run_step(h, batch, rows, hidden, **kw):
     return tok.cpu().numpy().astype(np.uint32), logits.cpu().numpy()
 
 
-def check_sampler_on_gpu_logits(rows, toks, logits, uniforms):
-    near = 0
-    for b, r in enumerate(rows):
-        p = oparams(r)
-        info = O.sample(logits[b], p, uniforms[b])
-        if int(toks[b]) == info.token:
-            continue
-        assert U.sample_near_tie(info, logits[b], p), (b, int(toks[b]), info.token, info.cut, info.rank)
-        near += 1
-    print(f"sampler-on-gpu-logits: {len(rows)} rows, {near} near-tie mismatches")
-    assert near <= max(1, len(rows) // 20)
+def check_sampler_on_gpu_logits(rows, toks, logits, uniforms, label="sampler-on-gpu-logits"):
+    """Every row's GPU token against the oracle sampler on the GPU's own final logits: inside its
+    CDF interval widened only by the GPU arithmetic's error bound (parity_util.draw_check, mode
+    "arith"), and equal to the oracle's token on all but a few rows."""
+    return U.check_tokens([oparams(r) for r in rows], toks, logits, uniforms, mode="arith", label=label)
+
+
+def check_chain_rows(rows, toks, want_logits, uniforms, label):
+    """GPU tokens against the oracle chain's own logits (which differ from the GPU's within the
+    logit tolerance): inside the token's CDF interval widened by the stated margin (1e-3 of r,
+    and of top_p for the nucleus). Rows that need the margin are counted and printed; a token
+    outside it fails."""
+    n = len(rows)
+    return U.check_tokens([oparams(r) for r in rows], toks, want_logits, uniforms, mode="margin",
+                          within_frac=1.0, label=label)
 
 
 def test_config1_greedy_b1(head):
@@ -72,49 +81,64 @@ def test_config1_greedy_b1(head):
         want_l, info = U.oracle_row(W, S, B, g, x[0], oparams(r), 0.0)
         err = np.abs(logits[0] - want_l)
         assert np.all(err <= 1e-5 + 1e-4 * np.abs(want_l)), float(err.max())
-        if U.greedy_near_tie(want_l):
-            print("config1: near tie, token not compared")
-            continue
-        assert int(toks[0]) == info.token == int(np.argmax(want_l))
+        assert int(toks[0]) == int(np.argmax(logits[0]))
+        res = U.draw_check(want_l, oparams(r), 0.0, int(toks[0]), mode="margin")
+        assert res == "exact" or U.greedy_near_tie(want_l), (step, res)
 
 
-def test_config2_sampled_b1_with_history(head):
-    """Config 2 over 128 consecutive decode steps (the reference's token-for-token gate,
-    CONTRIBUTING.md:37-47, on the sampled path): each step's logits against the oracle chain and
-    its token against the oracle's, the history growing on the device by each GPU token. The
-    replay is teacher-forced on the GPU's tokens, so a near-tie (counted) does not cascade."""
+CONFIG2_STEPS = 512
+CONFIG2_SEGMENT = 128
+_config2 = {}
+
+
+def _config2_state(h):
+    if not _config2:
+        hist0 = synth.uniform_ids(256, V, SEED)
+        hist = torch.zeros((1, 256 + CONFIG2_STEPS), dtype=torch.int32, device="cuda")
+        hist[0, :256] = torch.from_numpy(hist0.astype(np.int32))
+        _config2.update(hist=hist, hlen=torch.tensor([256], dtype=torch.int32, device="cuda"),
+                        host_hist=list(hist0), next=0, arith={"exact": 0, "within": 0},
+                        chain={"exact": 0, "within": 0}, worst=0.0)
+    return _config2
+
+
+@pytest.mark.parametrize("segment", range(CONFIG2_STEPS // CONFIG2_SEGMENT))
+def test_config2_sampled_b1_with_history(head, segment):
+    """Config 2 over its 512 consecutive decode steps (the reference's token-for-token gate,
+    CONTRIBUTING.md:37-47, on the sampled path), in four segments of 128 that continue one chain:
+    each step's logits against the oracle chain and its token against the oracle's, the history
+    growing on the device by each GPU token. The replay is teacher-forced on the GPU's tokens, so
+    a row decided inside the stated margin (counted) does not cascade. A segment run on its own
+    first runs the segments before it."""
     h, (W, S, B, g) = head
-    steps = 128
-    hist0 = synth.uniform_ids(256, V, SEED)
-    cap = 256 + steps
-    hist = torch.zeros((1, cap), dtype=torch.int32, device="cuda")
-    hist[0, :256] = torch.from_numpy(hist0.astype(np.int32))
-    hlen = torch.tensor([256], dtype=torch.int32, device="cuda")
-    host_hist = list(hist0)
-    mism = 0
-    worst = 0.0
-    for step in range(steps):
+    st = _config2_state(h)
+    end = (segment + 1) * CONFIG2_SEGMENT
+    while st["next"] < end:
+        step = st["next"]
         x = synth.hidden_states(1, D, SEED + 1, step)
         r = T.row_default(temperature=0.8, top_k=64, top_p=0.95, repetition_penalty=1.1,
                           seed=SEED, counter=step)
         u = T.row_uniform(r)
         assert u == O.philox_uniform(SEED, step)
         toks, logits = run_step(h, 1, [r], dev(x), flags=T.TURBO_STEP_APPEND_HISTORY,
-                                history=hist, history_len=hlen)
+                                history=st["hist"], history_len=st["hlen"])
         want_l, info = U.oracle_row(W, S, B, g, x[0], oparams(r), u,
-                                    history=np.array(host_hist, np.uint32))
+                                    history=np.array(st["host_hist"], np.uint32))
         err = U.logit_err(logits[0], want_l)
-        worst = max(worst, err)
+        st["worst"] = max(st["worst"], err)
         assert err <= 1e-4, (step, err)
-        check_sampler_on_gpu_logits([r], toks, logits, [u])
-        if int(toks[0]) != info.token:
-            assert U.sample_near_tie(info, want_l, oparams(r)), step
-            mism += 1
-        host_hist.append(int(toks[0]))
-    assert int(hlen.item()) == 256 + steps
-    assert np.array_equal(hist.cpu().numpy()[0, 256:].astype(np.uint32), np.array(host_hist[256:], np.uint32))
-    print(f"config2: {steps} steps, {mism} near-tie token mismatches, worst logit error {worst:.2e}")
-    assert mism <= max(1, steps // 32)
+        st["arith"][U.draw_check(logits[0], oparams(r), u, int(toks[0]), mode="arith")] += 1
+        st["chain"][U.draw_check(want_l, oparams(r), u, int(toks[0]), mode="margin")] += 1
+        st["host_hist"].append(int(toks[0]))
+        st["next"] += 1
+    n = st["next"]
+    assert int(st["hlen"].item()) == 256 + n
+    assert np.array_equal(st["hist"].cpu().numpy()[0, 256:256 + n].astype(np.uint32),
+                          np.array(st["host_hist"][256:], np.uint32))
+    print(f"config2 steps 0..{n - 1}: same logits {st['arith']}, oracle chain {st['chain']}, "
+          f"worst logit error {st['worst']:.2e}")
+    assert st["arith"]["within"] <= max(1, n // 32)
+    assert st["chain"]["within"] <= max(1, n // 32)
 
 
 def test_config3_mixed_b32(head):
@@ -134,12 +158,18 @@ def test_config3_mixed_b32(head):
     hl = torch.full((Bn,), 1024, dtype=torch.int32, device="cuda")
     toks, logits = run_step(h, Bn, rows, dev(x), history=dev(hists.astype(np.int32)), history_len=hl)
     us = [T.row_uniform(r) for r in rows]
-    check_sampler_on_gpu_logits(rows, toks, logits, us)
-    for b in (0, 3, 17, 30):
-        want_l, info = U.oracle_row(W, S, B, g, x[b], oparams(rows[b]), us[b], history=hists[b])
+    # every row, the eight top_k = 0 (full-vocabulary nucleus) rows among them
+    check_sampler_on_gpu_logits(rows, toks, logits, us, label="config3 same logits")
+    fv = [b for b in range(Bn) if ks[b % 4] == 0]
+    check_sampler_on_gpu_logits([rows[b] for b in fv], toks[fv], logits[fv], [us[b] for b in fv],
+                                label="config3 full-vocabulary rows")
+    chain = (0, 3, 17, 30)
+    want = []
+    for b in chain:
+        want_l, _ = U.oracle_row(W, S, B, g, x[b], oparams(rows[b]), us[b], history=hists[b])
         assert U.logit_err(logits[b], want_l) <= U.LOGIT_RTOL  # B > 2: fp16-dequant MFMA path
-        if int(toks[b]) != info.token:
-            assert U.sample_near_tie(info, want_l, oparams(rows[b])), b
+        want.append(want_l)
+    check_chain_rows([rows[b] for b in chain], toks[list(chain)], want, [us[b] for b in chain], "config3 chain")
 
 
 def test_config4_b256_full_vocab_nucleus(head):
@@ -151,25 +181,20 @@ def test_config4_b256_full_vocab_nucleus(head):
     toks, logits = run_step(h, Bn, rows, dev(xb.view(np.int16)), dtype=T.TURBO_HIDDEN_BF16,
                             flags=T.TURBO_STEP_NORMED)
     us = [T.row_uniform(r) for r in rows]
-    # every row: the GPU pick must sit on the oracle's CDF at r (flat distributions put most
-    # rows within the near-tie band, so check the interval itself)
-    for b in range(0, Bn, 8):
-        p = oparams(rows[b])
-        info = O.sample(logits[b], p, us[b])
-        if int(toks[b]) != info.token:
-            assert U.sample_near_tie(info, logits[b], p), b
-    # eight rows through the whole oracle chain: oracle logits, then the oracle sampler
-    near = 0
-    for b in (0, 37, 74, 111, 148, 185, 222, 255):
+    # all 256 rows: the GPU token inside its CDF interval on its own logits, up to the GPU
+    # arithmetic's bound, and the oracle's token on all but at most 1/8 of the rows
+    check_sampler_on_gpu_logits(rows, toks, logits, us, label="config4 same logits")
+    # eight rows through the whole oracle chain: oracle logits, then the oracle sampler; with
+    # ~160,000 survivors per row a logit difference inside the tolerance moves r across many
+    # tokens, so these rows are held to the stated margin around the token's interval
+    chain = (0, 37, 74, 111, 148, 185, 222, 255)
+    want = []
+    for b in chain:
         xf = synth.bf16_to_f32(xb[b])
         want_l = O.softcap(O.matvec(W, S, B, xf, U.THREADS), 30.0)
         assert U.logit_err(logits[b], want_l) <= U.LOGIT_RTOL
-        p = oparams(rows[b])
-        info = O.sample(want_l, p, us[b])
-        if int(toks[b]) != info.token:
-            assert U.sample_near_tie(info, want_l, p), b
-            near += 1
-    print(f"config4: 8 rows through the oracle chain, {near} near-tie token mismatches")
+        want.append(want_l)
+    check_chain_rows([rows[b] for b in chain], toks[list(chain)], want, [us[b] for b in chain], "config4 chain")
 
 
 def test_b256_logits_equal_b32_logits(head):
@@ -192,6 +217,36 @@ def test_b256_logits_equal_b32_logits(head):
         small = small.cpu().numpy()
         bad = np.nonzero((big[r0:r0 + 32].view(np.uint32) != small.view(np.uint32)).any(axis=1))[0]
         assert bad.size == 0, (r0, [int(r0 + i) for i in bad[:8]])
+
+
+DIGEST_FILE = Path(__file__).resolve().parent / "golden" / "logit_digests.json"
+
+
+@pytest.mark.parametrize("batch", [1, 2, 3, 32, 64, 256])
+def test_logit_bits_match_committed_digest(head, batch):
+    """Bit identity across refactors, the discipline of the reference's raw GEMV dumps
+    (tests/test_gpu_kernels.cpp:199-207, :260-266): the softcapped logits of fixed seeded rows
+    (normalised by the oracle, so only the head kernels are pinned) hash to the committed SHA-256
+    in tests/golden/logit_digests.json. The batch sizes cover every head kernel: the folded digit
+    kernel at one and two rows, and the matrix-core kernels at 32, 64 and 128 columns per
+    workgroup. A change that moves any bit updates the digest in the same commit, with the reason.
+    With TURBO_DIGEST_OUT set, the computed digests are also written to that JSON file."""
+    h, (W, S, B, g) = head
+    x = np.stack([O.rms_norm(r, g, 1e-6) for r in synth.hidden_states(batch, D, SEED + 50)])
+    out = torch.empty((batch, V), dtype=torch.float32, device="cuda")
+    h.logits(dev(x), batch, out)
+    h.sync()
+    got = hashlib.sha256(out.cpu().numpy().tobytes()).hexdigest()
+    key = f"b{batch}"
+    dump = os.environ.get("TURBO_DIGEST_OUT")
+    if dump:
+        p = Path(dump)
+        have = json.loads(p.read_text()) if p.exists() else {}
+        have[key] = got
+        p.parent.mkdir(parents=True, exist_ok=True)
+        p.write_text(json.dumps(have, indent=1, sort_keys=True) + "\n")
+    want = json.loads(DIGEST_FILE.read_text()).get("digests", {}) if DIGEST_FILE.exists() else {}
+    assert want.get(key) == got, (key, got)
 
 
 def test_config5_constrained_b64(head):
@@ -224,12 +279,14 @@ def test_config5_constrained_b64(head):
                                  bias_values=bvals[b], ban=bans[b])
         assert np.array_equal(logits[b], want), b
         assert np.all(np.isneginf(logits[b][np.unpackbits(bans[b].view(np.uint8), bitorder="little")[:V] == 1]))
-    for b in (1, 40):
-        want_l, info = U.oracle_row(W, S, B, g, x[b], oparams(rows[b]), us[b], history=hists[b],
-                                    bias_ids=bids[b], bias_values=bvals[b], ban=bans[b])
+    chain = (1, 40)
+    want = []
+    for b in chain:
+        want_l, _ = U.oracle_row(W, S, B, g, x[b], oparams(rows[b]), us[b], history=hists[b],
+                                 bias_ids=bids[b], bias_values=bvals[b], ban=bans[b])
         assert U.logit_err(logits[b], want_l) <= U.LOGIT_RTOL
-        if int(toks[b]) != info.token:
-            assert U.sample_near_tie(info, want_l, oparams(rows[b])), b
+        want.append(want_l)
+    check_chain_rows([rows[b] for b in chain], toks[list(chain)], want, [us[b] for b in chain], "config5 chain")
 
 
 # ---- sampler on given logits: shortlist, overflow and full-vocabulary paths ----------------------

@@ -84,3 +84,92 @@ def test_noalloc_rejects_inputs_past_its_scratch():
     inp, keep = T.LMHead.make_inputs(len(rows), rows)
     with pytest.raises(T.TurboError, match="batch must be in"):
         T.sample_logits_noalloc(lt, 16, inp, tok)
+
+
+def test_noalloc_allocates_nothing():
+    """Once the library has run, an eager call leaves the device's free memory unchanged (no
+    hipMalloc behind it; every buffer is caller-provided or the static array)."""
+    V, Bn, seed = 70001, 4, 14
+    base, rows, side = case(V, Bn, seed)
+    kw = dict(history=dev(side["history"].view(np.int32)), history_len=dev(side["history_len"]),
+              ban=dev(side["ban"].view(np.int32)), bias_ids=dev(side["bias_ids"].view(np.int32)),
+              bias_values=dev(side["bias_values"]), bias_count=dev(side["bias_count"]))
+    inp, keep = T.LMHead.make_inputs(Bn, rows, **kw)
+    lt = dev(base)
+    tok = torch.zeros(Bn, dtype=torch.int32, device="cuda")
+    T.sample_logits_noalloc(lt, V, inp, tok, softcap=30.0)  # the static array is set up by now
+    torch.cuda.synchronize()
+    lt.copy_(dev(base))
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info()
+    for _ in range(3):
+        T.sample_logits_noalloc(lt, V, inp, tok, softcap=30.0)
+    torch.cuda.synchronize()
+    free1, _ = torch.cuda.mem_get_info()
+    assert free1 == free0, (free0, free1)
+
+
+CAPTURE_CHILD = r"""
+import sys
+sys.path[:0] = {paths!r}
+import numpy as np, torch
+import turbo_decode_tail as T
+import test_zz_no_alloc as Z
+V, Bn, seed = 50021, 4, 15
+base, rows, side = Z.case(V, Bn, seed)
+kw = dict(history=Z.dev(side["history"].view(np.int32)), history_len=Z.dev(side["history_len"]),
+          ban=Z.dev(side["ban"].view(np.int32)), bias_ids=Z.dev(side["bias_ids"].view(np.int32)),
+          bias_values=Z.dev(side["bias_values"]), bias_count=Z.dev(side["bias_count"]))
+inp, keep = T.LMHead.make_inputs(Bn, rows, **kw)
+lt = Z.dev(base)
+tok = torch.zeros(Bn, dtype=torch.int32, device="cuda")
+rep = torch.zeros((Bn, 14), dtype=torch.int32, device="cuda")
+torch.cuda.synchronize()
+# the process's FIRST call of the entry point is the captured one: the array's address lookup
+# and its clear (a fill kernel, recorded as a graph node) happen under capture
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g):
+    T.sample_logits_noalloc(lt, V, inp, tok, rep, softcap=30.0, stream=torch.cuda.current_stream().cuda_stream)
+torch.cuda.synchronize()
+# the eager result of the handle sampler on the same inputs
+W, S, B, _ = Z.synth.make_head(V, Z.D, seed)
+h = T.LMHead(W, S, B, None, vocab=V, hidden=Z.D, softcap=30.0)
+t0, l0, r0 = Z.run(lambda lt_, i, t, r: h.sample_logits(lt_, i, t, r), base, rows, side)
+h.close()
+bad = 0
+for replay in range(3):
+    lt.copy_(Z.dev(base))           # eager work between replays
+    tok.zero_(); rep.zero_()
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    same = (np.array_equal(tok.cpu().numpy(), t0) and np.array_equal(rep.cpu().numpy(), r0)
+            and np.array_equal(lt.cpu().numpy().view(np.uint32), l0.view(np.uint32)))
+    print(f"replay {{replay}}: {{'equal' if same else 'DIFFERENT'}} tokens {{tok.cpu().numpy().tolist()}}", flush=True)
+    bad += 0 if same else 1
+# an eager call after the captured ones (the array is cleared again outside capture)
+t1, l1, r1 = Z.run(lambda lt_, i, t, r: T.sample_logits_noalloc(lt_, V, i, t, r, softcap=30.0), base, rows, side)
+same = np.array_equal(t1, t0) and np.array_equal(r1, r0) and np.array_equal(l1.view(np.uint32), l0.view(np.uint32))
+print(f"eager after replays: {{'equal' if same else 'DIFFERENT'}}", flush=True)
+bad += 0 if same else 1
+sys.exit(1 if bad else 0)
+"""
+
+
+def test_noalloc_first_call_under_graph_capture():
+    """The use the entry point exists for: a call recorded into a HIP graph (torch's global capture
+    mode, under which any hipMalloc fails) and replayed. Run in a fresh process so that the
+    recorded call is the process's first, taking the array's set-up path under capture; every
+    replay and a later eager call must equal the handle sampler's eager result bit for bit."""
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = Path(__file__).resolve().parents[1]
+    paths = [str(root / "turbo-winfare_amd"), str(root / "oracle"), str(root / "tests")]
+    code = CAPTURE_CHILD.format(paths=paths)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300,
+                       env=dict(os.environ))
+    print(r.stdout)
+    assert r.returncode == 0, (r.returncode, r.stdout[-2000:], r.stderr[-2000:])
+    assert r.stdout.count("equal") >= 4 and "DIFFERENT" not in r.stdout

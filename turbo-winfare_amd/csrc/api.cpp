@@ -66,6 +66,19 @@ void dfree(void* p) {
     if (p) (void)hipFree(p);
 }
 
+// The private stream of turbo_lmhead_create: drained and destroyed on every way out.
+struct CreateStream {
+    hipStream_t s = nullptr;
+    void drain() {
+        if (s) {
+            (void)hipStreamSynchronize(s);
+            (void)hipStreamDestroy(s);
+            s = nullptr;
+        }
+    }
+    ~CreateStream() { drain(); }
+};
+
 // ---- host restatement of the reference's scalar sampling helpers ---------------------------
 
 uint64_t splitmix64_h(uint64_t x) {  // src/sampling.cpp:56-61
@@ -138,8 +151,9 @@ bool validate_row(const TurboSamplingRow& p, std::string* why) {
     return true;
 }
 
+// Waits for the handle's own stream only (other streams of the process keep running), then frees.
 void free_head(Head& h) {
-    if (h.stream || h.Wt) (void)hipDeviceSynchronize();
+    (void)hipStreamSynchronize(h.stream);
     dfree(h.Wt);
     dfree(h.SBt);
     dfree(h.gamma);
@@ -148,6 +162,7 @@ void free_head(Head& h) {
     dfree(h.xws);
     dfree(h.xsum);
     dfree(h.x16);
+    dfree(h.xscale);
     dfree(h.SB16t);
     dfree(h.logits);
     dfree(h.partials);
@@ -211,6 +226,7 @@ tdt::PrepArgs prep_args(const Head& h, int B) {
     a.xsum = h.xsum;
     a.x16 = h.x16;
     a.x16_denorm = h.mfma_denorm ? 1 : 0;
+    a.xscale = h.xscale;
     a.V = h.V;
     a.ntile = h.ntile;
     a.P = 2;
@@ -279,6 +295,7 @@ tdt::EpiArgs epi_args(const Head& h, float* logits, bool softcap) {
     ep.ban_stride = 0;
     ep.rep_limit = (h.cap > 0.0f) ? h.cap * 0.9999f : 0.0f;
     ep.no_sumexp = 1u;  // the sampling step sets 0 when a row samples from a shortlist
+    ep.xscale = h.xscale;
     return ep;
 }
 
@@ -306,6 +323,14 @@ void launch_head(HandleBox& bx, int B, const tdt::EpiArgs& ep, const tdt::FusedP
 
 tdt::HeadPath path_for(int B) { return B <= 2 ? tdt::HeadPath::Digits : tdt::HeadPath::Mfma; }
 
+// Batches above two rows run on the matrix cores, whose fp16 table cannot hold scales or biases
+// beyond the fp16 range; such a head serves one- and two-row calls only.
+void check_head_path(const Head& h, int B) {
+    if (B > 2 && !h.mfma_ok)
+        throw std::runtime_error("this head's scales or biases exceed the fp16 range (|x| > 65504), which the "
+                                 "matrix-core path for batches above 2 rows cannot represent; call with batch <= 2");
+}
+
 // The head over normalised rows x with greedy row parameters (turbo_lmhead_logits,
 // turbo_int4_matvec, turbo_lmhead_greedy). One or two 16-byte-aligned rows: the head kernel
 // computes the digit planes itself (no preparation kernel), with one workgroup per 16 tiles or,
@@ -313,6 +338,7 @@ tdt::HeadPath path_for(int B) { return B <= 2 ? tdt::HeadPath::Digits : tdt::Hea
 void launch_greedy_head(HandleBox& bx, const tdt::DevRow* rows, int batch, const void* x, int x_dtype,
                         const tdt::EpiArgs& ep) {
     Head& h = bx.h;
+    check_head_path(h, batch);
     const uint32_t nt = tdt::split_threads(h);
     const bool fold = batch <= tdt::kFusedRows && h.D <= tdt::kFusedMaxD &&
                       (reinterpret_cast<uintptr_t>(x) & 15u) == 0u &&
@@ -349,6 +375,7 @@ int run_rows(Head& h, HandleBox* bx, const TurboStepInputs* in, const TurboStepO
     if (hidden && !bx) throw std::runtime_error("a head step needs a handle");
     const int B = in->batch;
     check_batch(h, B);
+    if (hidden) check_head_path(h, B);
     if (!in->rows) throw std::runtime_error("rows is NULL");
     if (!out->tokens) throw std::runtime_error("out->tokens is NULL");
     if (hidden && in->hidden_dtype != TURBO_HIDDEN_F32 && in->hidden_dtype != TURBO_HIDDEN_BF16)
@@ -514,6 +541,20 @@ extern "C" {
 
 TURBO_DT_API const char* turbo_lmhead_last_error(void) { return g_last_error.c_str(); }
 
+TURBO_DT_API uint32_t turbo_abi_version(void) { return TURBO_DT_ABI_VERSION; }
+
+TURBO_DT_API size_t turbo_abi_struct_size(int which) {
+    switch (which) {
+        case TURBO_ABI_LMHEAD_DESC: return sizeof(TurboLMHeadDesc);
+        case TURBO_ABI_BUNDLE_TENSOR: return sizeof(TurboBundleTensor);
+        case TURBO_ABI_SAMPLING_ROW: return sizeof(TurboSamplingRow);
+        case TURBO_ABI_STEP_INPUTS: return sizeof(TurboStepInputs);
+        case TURBO_ABI_ROW_REPORT: return sizeof(TurboRowReport);
+        case TURBO_ABI_STEP_OUTPUTS: return sizeof(TurboStepOutputs);
+        default: return 0;
+    }
+}
+
 TURBO_DT_API void turbo_lmhead_desc_default(TurboLMHeadDesc* out) {
     if (!out) return;
     std::memset(out, 0, sizeof(*out));
@@ -541,6 +582,7 @@ TURBO_DT_API void* turbo_lmhead_create(const TurboLMHeadDesc* d) {
 
     auto bx = std::make_unique<HandleBox>();
     Head& h = bx->h;
+    CreateStream cs;
     try {
         int ndev = 0;
         check_hip(hipGetDeviceCount(&ndev), "hipGetDeviceCount");
@@ -557,6 +599,8 @@ TURBO_DT_API void* turbo_lmhead_create(const TurboLMHeadDesc* d) {
         h.stream = nullptr;
         h.max_batch = kMaxBatch;
         h.mod_cap = tdt::kModCap;
+        // create-time uploads, clears and repacks run on a stream of their own, awaited at the end
+        check_hip(hipStreamCreateWithFlags(&cs.s, hipStreamNonBlocking), "create stream");
 
         const size_t wbytes = static_cast<size_t>(h.V) * (h.D / 2u);
         const size_t gcount = static_cast<size_t>(h.V) * h.G;
@@ -574,22 +618,24 @@ TURBO_DT_API void* turbo_lmhead_create(const TurboLMHeadDesc* d) {
             tW = dalloc<uint8_t>(wbytes, "alloc staging W");
             tS = dalloc<uint16_t>(gcount, "alloc staging S");
             tB = dalloc<uint16_t>(gcount, "alloc staging B");
-            check_hip(hipMemcpy(tW, d->weight, wbytes, hipMemcpyHostToDevice), "upload W");
-            check_hip(hipMemcpy(tS, d->scales, gcount * 2, hipMemcpyHostToDevice), "upload S");
-            check_hip(hipMemcpy(tB, d->biases, gcount * 2, hipMemcpyHostToDevice), "upload B");
+            check_hip(hipMemcpyAsync(tW, d->weight, wbytes, hipMemcpyHostToDevice, cs.s), "upload W");
+            check_hip(hipMemcpyAsync(tS, d->scales, gcount * 2, hipMemcpyHostToDevice, cs.s), "upload S");
+            check_hip(hipMemcpyAsync(tB, d->biases, gcount * 2, hipMemcpyHostToDevice, cs.s), "upload B");
             W = tW;
             S = tS;
             Bi = tB;
         }
-        h.mfma_denorm = tdt::launch_repack(h, W, S, Bi, nullptr);
+        const int repack = tdt::launch_repack(h, W, S, Bi, cs.s);  // waits for cs.s
+        h.mfma_denorm = repack == 1;
+        h.mfma_ok = repack >= 0;
         dfree(tW);
         dfree(tS);
         dfree(tB);
 
         if (d->norm_weight) {
             h.gamma = dalloc<uint16_t>(h.D, "alloc gamma");
-            check_hip(hipMemcpy(h.gamma, d->norm_weight, h.D * 2u,
-                                d->weights_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice),
+            check_hip(hipMemcpyAsync(h.gamma, d->norm_weight, h.D * 2u,
+                                     d->weights_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, cs.s),
                       "upload gamma");
         }
         const size_t MB = static_cast<size_t>(h.max_batch);
@@ -598,6 +644,9 @@ TURBO_DT_API void* turbo_lmhead_create(const TurboLMHeadDesc* d) {
         h.xws = dalloc<float>(MB * h.G, "alloc xws");
         h.xsum = dalloc<float>(MB * h.G, "alloc xsum");
         h.x16 = dalloc<uint16_t>(MB * h.D, "alloc x16");
+        h.xscale = dalloc<float>(MB, "alloc xscale");
+        check_hip(hipMemsetD32Async(reinterpret_cast<hipDeviceptr_t>(h.xscale), 0x3f800000, MB, cs.s),
+                  "clear xscale");  // 1.0f
         h.logits = dalloc<float>(MB * h.V, "alloc logits");
         h.partials = dalloc<tdt::BlockPartial>(MB * h.ntile, "alloc partials");
         h.rows = dalloc<tdt::DevRow>(MB, "alloc rows");
@@ -607,17 +656,18 @@ TURBO_DT_API void* turbo_lmhead_create(const TurboLMHeadDesc* d) {
         h.hbw = (h.V + 31u) / 32u;
         h.hcount = dalloc<uint32_t>(MB * h.V, "alloc history counts");
         h.hbits = dalloc<uint32_t>(MB * h.hbw, "alloc history bitmap");
-        check_hip(hipMemset(h.hcount, 0, MB * h.V * sizeof(uint32_t)), "clear history counts");
-        check_hip(hipMemset(h.hbits, 0, MB * h.hbw * sizeof(uint32_t)), "clear history bitmap");
+        check_hip(hipMemsetAsync(h.hcount, 0, MB * h.V * sizeof(uint32_t), cs.s), "clear history counts");
+        check_hip(hipMemsetAsync(h.hbits, 0, MB * h.hbw * sizeof(uint32_t), cs.s), "clear history bitmap");
         h.list_scratch = dalloc<uint2>(MB * h.V, "alloc list scratch");
         h.fv_acc = dalloc<unsigned long long>((size_t)tdt::kFvMaxBatch * 2u * tdt::kFvBins,
                                               "alloc select slice-histogram sums");
-        check_hip(hipMemset(h.fv_acc, 0, (size_t)tdt::kFvMaxBatch * 2u * tdt::kFvBins * 8u),
+        check_hip(hipMemsetAsync(h.fv_acc, 0, (size_t)tdt::kFvMaxBatch * 2u * tdt::kFvBins * 8u, cs.s),
                   "clear select slice-histogram sums");
         h.fv_merged = dalloc<unsigned long long>((size_t)tdt::kFvMaxBatch * 2u * tdt::kFvBins, "alloc select histograms");
         h.fv_cand = dalloc<unsigned long long>((size_t)tdt::kFvMaxBatch * tdt::kFvCandCap, "alloc select candidates");
         h.fv_state = dalloc<unsigned char>((size_t)tdt::kFvMaxBatch * tdt::kFvStateBytes, "alloc select state");
-        check_hip(hipMemset(h.fv_state, 0, (size_t)tdt::kFvMaxBatch * tdt::kFvStateBytes), "clear select state");
+        check_hip(hipMemsetAsync(h.fv_state, 0, (size_t)tdt::kFvMaxBatch * tdt::kFvStateBytes, cs.s),
+                  "clear select state");
         check_hip(hipHostMalloc(reinterpret_cast<void**>(&h.ring_host),
                                 sizeof(tdt::DevRow) * MB * Head::kRing,
                                 hipHostMallocMapped | hipHostMallocCoherent),
@@ -632,8 +682,9 @@ TURBO_DT_API void* turbo_lmhead_create(const TurboLMHeadDesc* d) {
         *h.overflow_host = 0u;
         check_hip(hipHostGetDevicePointer(reinterpret_cast<void**>(&h.overflow_dev), h.overflow_host, 0),
                   "map history overflow word");
-        check_hip(hipDeviceSynchronize(), "create");
+        check_hip(hipStreamSynchronize(cs.s), "create");
     } catch (...) {
+        cs.drain();
         free_head(h);
         throw;
     }

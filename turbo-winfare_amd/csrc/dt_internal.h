@@ -38,6 +38,9 @@ struct Head {
     // denormals), else fp16(s) | fp16(b) << 16 (the dequant through the mantissa of 1024.0).
     uint32_t* SB16t = nullptr;
     bool mfma_denorm = true;
+    // false when some scale or bias lies outside the fp16 range even unscaled: the matrix-core
+    // path cannot represent the table, and batches above two rows fail with an error
+    bool mfma_ok = true;
     uint16_t* gamma = nullptr;   // [D] bf16 or null
 
     int max_batch = 0;
@@ -49,6 +52,7 @@ struct Head {
     float* xws = nullptr;        // [max_batch][G] block-fp scale 2^(e-21)
     float* xsum = nullptr;       // [max_batch][G] sum of the block-fp activations
     uint16_t* x16 = nullptr;     // [max_batch][D] fp16, k-permuted within octets (MFMA path)
+    float* xscale = nullptr;     // [max_batch] 2^k: x16 holds row b times 2^-k (MFMA path)
     float* logits = nullptr;     // [max_batch][V] scratch logits
     BlockPartial* partials = nullptr;  // [max_batch][ntile]
     DevRow* rows = nullptr;      // [max_batch]
@@ -113,6 +117,8 @@ struct EpiArgs {
                                // largest values are not needed (left -inf by the MFMA head)
     uint32_t meta;             // 1: some row has modifiers or a ban mask (the MFMA head stages
                                // their words in LDS); 0: the MFMA head skips modifiers and ban
+    const float* xscale;       // [B] the MFMA head multiplies row b's accumulators by xscale[b]
+                               // (the power of two its fp16 activations were scaled down by)
 };
 
 enum class HeadPath { Digits, Mfma };
@@ -139,6 +145,7 @@ struct PrepArgs {
     float* xsum;
     uint16_t* x16;
     int x16_denorm;              // fp16 layout: (16 x, x) per (even, odd) element, else (x, x / 16)
+    float* xscale;               // [B] 2^k when row b is stored in x16 as x * 2^-k (fp16 path)
     // history counts and the bias table
     uint32_t V, ntile, P;        // P: bias sort size (power of two >= bias_stride)
     uint32_t* hcount;
@@ -158,10 +165,11 @@ struct PrepArgs {
     uint32_t mod_bits[16];       // 2 bits per row (DevRow::has_mods), so no block reads the
                                  // host-mapped staging slot except the row copy
 };
-// Fills Wt, SBt and SB16t; returns whether every scale fits the denormal dequant (|s| < 1/16),
-// in which case SB16t holds s * 2^20, else s (synchronises).
-bool launch_repack(const Head& h, const uint8_t* W, const uint16_t* S, const uint16_t* B,
-                   hipStream_t st);
+// Fills Wt, SBt and SB16t on st and waits for it. Returns 1 when every scale fits the denormal
+// dequant (|s| < 1/16; SB16t holds s * 2^20), 0 when SB16t holds s, and -1 when some scale or
+// bias is outside the fp16 range either way (the matrix-core path cannot use the table).
+int launch_repack(const Head& h, const uint8_t* W, const uint16_t* S, const uint16_t* B,
+                  hipStream_t st);
 void launch_step_prep(const Head& h, const PrepArgs& a, bool with_mods, hipStream_t st);
 uint32_t modtable_sort_size(const Head& h, uint32_t n);
 

@@ -37,8 +37,11 @@ __device__ inline uint32_t magic_vgpr() {
 
 // 8 nibbles -> 8 halves in the order (e0, e4, e1, e5, e2, e6, e3, e7), e = round16(q s + b) (one
 // rounding: every product below is exact), the even elements divided by 16 and their activation
-// slots holding 16 x (power-of-two scaling commutes with the rounding), so that each product is
-// exactly the intended round16(q s + b) * x. Two ways to make the fp16 operand of q:
+// slots holding 16 x. Power-of-two scaling commutes with the rounding while the value stays in
+// the fp16 normal range, so each product is then exactly round16(q s + b) * x. An even element
+// with |q s + b| / 16 below 2^-14 (|q s + b| < 2^-10) rounds on the fp16 subnormal grid instead:
+// its product is off by at most 2^-25 * 16 |x| = 2^-21 |x|, the same absolute size as the normal
+// range's 2^-11 relative error at that magnitude. Two ways to make the fp16 operand of q:
 //   DENORM: the nibbles are used where they lie. Masked in place, an even nibble (bits 0-3 of a
 //     half) is the fp16 denormal q * 2^-24 and an odd one (bits 4-7) q * 2^-20; with s2 = s * 2^20,
 //     (q 2^-20)(s 2^20) = q s and (q 2^-24)(s 2^20) = q s / 16. 9 VALU instructions per 8

@@ -21,8 +21,10 @@
 //    buffer loads; the activations reach a ring in LDS by buffer-to-LDS DMA, PF - 1 groups
 //    ahead, a group's DMA instructions spread over its k-steps, with one wait and one barrier
 //    per group.
-//  * Epilogue in place on the accumulators: per (column, 64-row tile), lane-local reductions
-//    and one cross-lane exchange give the block partial; logits leave as float4 stores.
+//  * Epilogue in place on the accumulators: a row whose activations were stored scaled by 2^-k
+//    (its largest |x| above 2^11, step prep) has its accumulators multiplied by 2^k first; then
+//    per (column, 64-row tile), lane-local reductions and one cross-lane exchange give the block
+//    partial; logits leave as float4 stores.
 #include <hip/hip_ext.h>
 
 #include <stdexcept>
@@ -313,6 +315,14 @@ __global__ __launch_bounds__(64 * WV, OCC) void k_head_mfma(
             __builtin_amdgcn_s_barrier();
         }
     }
+    // Per column, the power of two that undoes the row scaling of its fp16 activations (1 for
+    // every row within the fp16 range), loaded under the wait that drains the ring.
+    float csc[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        const uint32_t c = cbase + 32u * (uint32_t)nb + l32;
+        csc[nb] = (ep.xscale && c < B) ? ep.xscale[c] : 1.0f;
+    }
     // The clamped DMAs past the last group may still be writing the ring; the epilogue reuses it.
     __builtin_amdgcn_s_waitcnt(vm_wait(0u));
     __builtin_amdgcn_s_barrier();
@@ -337,6 +347,10 @@ __global__ __launch_bounds__(64 * WV, OCC) void k_head_mfma(
         for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) zz[16 * mb + r] = acc[mb][nb][r];
+        if (csc[nb] != 1.0f) {
+#pragma unroll
+            for (int i = 0; i < 32; ++i) zz[i] *= csc[nb];
+        }
         if (ep.cap > 0.0f) softcap_values<32>(zz, sc, ep.cap);
         bool may_ninf = !full_tile;  // some value may be -inf (padding, ban, a -inf bias)
         if constexpr (META) {

@@ -23,6 +23,18 @@ struct MatrixBox {
     uint32_t rows = 0, D = 0, G = 0, NC = 0, ntile = 0;
     uint4* Wt = nullptr;
     uint32_t* SBt = nullptr;
+    // the streams this matrix's loads and products were enqueued on, waited for by destroy (more
+    // than kStreams distinct streams: destroy waits for the whole device)
+    static constexpr int kStreams = 4;
+    hipStream_t used[kStreams] = {};
+    int nused = 0;
+    bool many = false;
+    void note(hipStream_t st) {
+        for (int i = 0; i < nused; ++i)
+            if (used[i] == st) return;
+        if (nused < kStreams) used[nused++] = st;
+        else many = true;
+    }
 };
 
 MatrixBox* mbox(void* p) {
@@ -93,6 +105,7 @@ TURBO_DT_API int turbo_int4_matrix_load(void* handle, const uint8_t* weight, con
     if (!weight || !scales || !biases) throw std::runtime_error("weight/scales/biases are NULL");
     tdt::check_hip(hipSetDevice(m->device), "hipSetDevice");
     hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    m->note(st);
     const size_t wbytes = (size_t)m->rows * (m->D / 2u), gcount = (size_t)m->rows * m->G;
     if (weights_on_device) {
         // the slot's bytes are repacked in place of the previous contents, stream-ordered
@@ -129,7 +142,11 @@ TURBO_DT_API void turbo_int4_matrix_destroy(void* handle) {
     try {
         MatrixBox* m = mbox(handle);
         (void)hipSetDevice(m->device);
-        (void)hipDeviceSynchronize();
+        if (m->many) {
+            (void)hipDeviceSynchronize();
+        } else {
+            for (int i = 0; i < m->nused; ++i) (void)hipStreamSynchronize(m->used[i]);
+        }
         free_matrix(*m);
         m->magic = 0;
         delete m;
@@ -156,6 +173,7 @@ TURBO_DT_API int turbo_int4_matvec_grouped(void* const* matrices, int count, con
         if (!x[i] || !out[i]) throw std::runtime_error("x[" + std::to_string(i) + "] or out[" + std::to_string(i) + "] is NULL");
         if ((reinterpret_cast<uintptr_t>(x[i]) & 15u) != 0u)
             throw std::runtime_error("x[" + std::to_string(i) + "] must be 16-byte aligned");
+        m->note(static_cast<hipStream_t>(hip_stream));
         tdt::GroupMat& g = a.m[i];
         g.Wt = m->Wt;
         g.SBt = m->SBt;

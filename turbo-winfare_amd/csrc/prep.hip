@@ -65,7 +65,7 @@ __global__ void k_repack_sb16(const uint16_t* __restrict__ S, const uint16_t* __
         const _Float16 hs = (_Float16)bf16_to_f32(S[row * G + g]);
         const _Float16 hm = (_Float16)((float)hs * mul);
         const _Float16 hb = (_Float16)bf16_to_f32(B[row * G + g]);
-        if (!__builtin_isfinite((float)hm)) atomicOr(bad, 1u);
+        if (!__builtin_isfinite((float)hm) || !__builtin_isfinite((float)hb)) atomicOr(bad, 1u);
         v = (uint32_t)__builtin_bit_cast(uint16_t, hm) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
     }
     SB16t[it] = v;
@@ -84,8 +84,8 @@ void launch_repack_table(uint4* Wt, uint32_t* SBt, uint32_t V, uint32_t NC, uint
     check_hip(hipGetLastError(), "repack scales");
 }
 
-bool launch_repack(const Head& h, const uint8_t* W, const uint16_t* S, const uint16_t* B,
-                   hipStream_t st) {
+int launch_repack(const Head& h, const uint8_t* W, const uint16_t* S, const uint16_t* B,
+                  hipStream_t st) {
     launch_repack_table(h.Wt, h.SBt, h.V, h.NC, h.G, h.ntile, W, S, B, st);
     const uint64_t items_sb = (uint64_t)h.ntile * h.G * kTileRows;
     const uint32_t tpb = 256;
@@ -108,7 +108,8 @@ bool launch_repack(const Head& h, const uint8_t* W, const uint16_t* S, const uin
     if (e == hipSuccess && !denorm) e = fill(1.0f, &flag);
     (void)hipFree(bad);
     check_hip(e, "repack fp16 scales");
-    return denorm;
+    if (denorm) return 1;
+    return flag == 0u ? 0 : -1;
 }
 
 // ---- per-step preparation (one launch) -------------------------------------------------------
@@ -130,7 +131,12 @@ bool launch_repack(const Head& h, const uint8_t* W, const uint16_t* S, const uin
 // fp16 (MFMA path): x rounded to fp16 and stored k-permuted within each octet as
 // (x0, x4, x1, x5, x2, x6, x3, x7), the order in which the weight dequant produces halves, with
 // the even elements times 16 (denormal dequant, whose even weight halves carry 1/16) or the odd
-// elements divided by 16 (the other dequant, whose odd weight halves carry 16).
+// elements divided by 16 (the other dequant, whose odd weight halves carry 16). A row whose
+// largest |x| exceeds 2^11 (where 16 x would approach the fp16 maximum, 65504) is stored as
+// x * 2^-k, k the smallest shift that brings it to 2^11 or below, and xscale[b] = 2^k tells the
+// head epilogue to multiply the row's fp32 accumulators back. A power of two commutes with fp16
+// and fp32 rounding in their normal ranges, so the logits are those of an fp16 format without
+// an exponent limit; rows within range (k = 0, every normalised hidden state) are unchanged.
 //
 // History counts: the occurrences of each id < V (merged per id in LDS first) are added to
 // hcount[b][id] and the id's bit is set in hbits[b] (global atomics); the head epilogue zeroes
@@ -155,6 +161,7 @@ static_assert(kHistSlots <= kPrepPoolU64, "the history table lives in the prep k
 __device__ void prep_row(const PrepArgs& a, uint32_t b, uint32_t k) {
 #pragma clang fp contract(off)
     __shared__ double red[kPrepWaves];
+    __shared__ float redm[kPrepWaves];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t D = a.D;
     const uint32_t i = k * kPrepThreads + tid;  // this thread's element
@@ -175,6 +182,9 @@ __device__ void prep_row(const PrepArgs& a, uint32_t b, uint32_t k) {
 #pragma unroll
     for (uint32_t q = 1; q < kPer; ++q)
         if (q == k) v = xv[q];
+    // fp16 path: the largest |normalised x| of the row, every block of the row computing it the
+    // same way from the same values
+    float rmax = 0.0f;
     if (!a.normed) {
         // src/cpu_reference.cpp:44-46: double sum of squares, float mean + eps, 1/sqrt.
         double acc = 0.0;
@@ -191,6 +201,29 @@ __device__ void prep_row(const PrepArgs& a, uint32_t b, uint32_t k) {
         const float inv = (float)(1.0 / (double)sq);
         v = v * inv;
         if (a.gamma) v = v * gw;
+        if (a.path == 1) {
+#pragma unroll
+            for (uint32_t q = 0; q < kPer; ++q) {
+                const uint32_t j = tid + q * kPrepThreads;
+                float t = xv[q] * inv;
+                if (a.gamma && j < D) t = t * bf16_to_f32(a.gamma[j]);
+                rmax = fmaxf(rmax, fabsf(t));
+            }
+        }
+    } else if (a.path == 1) {
+#pragma unroll
+        for (uint32_t q = 0; q < kPer; ++q) rmax = fmaxf(rmax, fabsf(xv[q]));
+    }
+    int shift = 0;  // the row is stored in fp16 as x * 2^-shift
+    if (a.path == 1) {
+        rmax = wave_max(rmax);
+        if (lane == 0) redm[wave] = rmax;
+        __syncthreads();
+        rmax = wave_max(lane < kPrepWaves ? redm[lane] : 0.0f);
+        int e = 0;
+        (void)frexpf(rmax, &e);  // rmax = f * 2^e, f in [0.5, 1)
+        if (__builtin_isfinite(rmax) && e > 11) shift = e - 11;
+        if (k == 0u && tid == 0u && a.xscale) a.xscale[b] = ldexpf(1.0f, shift);
     }
     if (i >= D) return;  // whole waves: D is a multiple of the 64-element group
     if (a.xn) a.xn[(size_t)b * D + i] = v;
@@ -222,6 +255,7 @@ __device__ void prep_row(const PrepArgs& a, uint32_t b, uint32_t k) {
     } else {
         const uint32_t e = i & 7u;
         const uint32_t slot = (e < 4u) ? 2u * e : 2u * (e - 4u) + 1u;
+        if (shift) v = ldexpf(v, -shift);
         const _Float16 hv = (_Float16)(a.x16_denorm ? ((e & 1u) ? v : v * 16.0f) : ((e & 1u) ? v * 0.0625f : v));
         a.x16[(size_t)b * D + (i & ~7u) + slot] = __builtin_bit_cast(uint16_t, hv);
     }

@@ -25,6 +25,8 @@ TURBO_STATUS_HISTORY_FULL = 1
 
 # Every symbol include/turbo_decode_tail.h declares.
 EXPORTS = (
+    "turbo_abi_version",
+    "turbo_abi_struct_size",
     "turbo_lmhead_last_error",
     "turbo_lmhead_desc_default",
     "turbo_lmhead_create",
@@ -171,6 +173,8 @@ def load(path: os.PathLike | str | None = None) -> C.CDLL:
     lib = C.CDLL(str(p))
     vp, u32, i32, f32 = C.c_void_p, C.c_uint32, C.c_int, C.c_float
     sig = {
+        "turbo_abi_version": (u32, []),
+        "turbo_abi_struct_size": (C.c_size_t, [i32]),
         "turbo_lmhead_last_error": (C.c_char_p, []),
         "turbo_lmhead_desc_default": (None, [C.POINTER(TurboLMHeadDesc)]),
         "turbo_lmhead_create": (vp, [C.POINTER(TurboLMHeadDesc)]),
