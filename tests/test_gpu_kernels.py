@@ -126,15 +126,21 @@ def test_step_normed_large_activations(small_head):
     x[3] *= 5.0e3 / np.abs(x[3]).max()
     x = x.astype(np.float32)
     rows = [T.row_default() for _ in range(Bn)]
-    inp, keep = h.make_inputs(Bn, rows, hidden=dev(x), flags=T.TURBO_STEP_NORMED)
+    xd = dev(x)  # kept alive: the inputs hold its raw device pointer
+    inp, keep = h.make_inputs(Bn, rows, hidden=xd, flags=T.TURBO_STEP_NORMED)
     tok = torch.zeros(Bn, dtype=torch.int32, device="cuda")
     lg = torch.empty((Bn, V_SMALL), dtype=torch.float32, device="cuda")
     h.step(inp, tok, lg)
     h.sync()
     got, toks = lg.cpu().numpy(), tok.cpu().numpy()
     for b in range(Bn):
-        want = O.softcap(O.matvec(W, S, B, x[b], U.THREADS), 30.0)
-        assert U.logit_err(got[b], want) <= U.LOGIT_RTOL, b
+        raw = O.matvec(W, S, B, x[b], U.THREADS)
+        want = O.softcap(raw, 30.0)
+        # the tolerance is set on the raw logits (their RMS is ~1e4 for the large rows) and carries
+        # through the softcap, whose slope is at most 1
+        scale = np.maximum(np.abs(raw), np.sqrt(np.mean(raw.astype(np.float64) ** 2)))
+        err = np.abs(got[b].astype(np.float64) - want) / scale
+        assert np.all(np.isfinite(got[b])) and float(err.max()) <= U.LOGIT_RTOL, (b, float(err.max()))
         assert U.draw_check(want, O.params(0.0), 0.0, int(toks[b]), mode="margin") in ("exact", "within")
 
 

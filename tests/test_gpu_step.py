@@ -246,6 +246,8 @@ def test_logit_bits_match_committed_digest(head, batch):
         p.parent.mkdir(parents=True, exist_ok=True)
         p.write_text(json.dumps(have, indent=1, sort_keys=True) + "\n")
     want = json.loads(DIGEST_FILE.read_text()).get("digests", {}) if DIGEST_FILE.exists() else {}
+    if dump and key not in want:
+        pytest.skip(f"{key}: no committed digest yet; wrote {got} to {dump}")
     assert want.get(key) == got, (key, got)
 
 
