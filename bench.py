@@ -26,7 +26,8 @@ B*D*(4 fp32 | 2 bf16) + the side inputs (history 4 B/id, ban 32,768 B/row, bias 
 cpu_baseline: the oracle's C restatement of the reference CPU path (src/cpu_reference.cpp
 RMSNorm/matvec/softcap + src/sampling.cpp penalty/sampler) for config-2 steps, timed inside C
 (CLOCK_MONOTONIC per step, median) at 1 thread and at the host's nproc threads (capped at the 16
-CPUs one GPU's job may use).
+CPUs one GPU's job may use). parity: those CPU steps' tokens against the GPU line's first steps,
+which ran on identical inputs ({"steps", "equal", "near_ties", "first_mismatch"}).
 """
 from __future__ import annotations
 
@@ -358,13 +359,39 @@ def cpu_baseline(W, S, B, g, one_steps=5, many_steps=16):
     toks1, med1 = run(1, one_steps)
     toksn, medn = run(threads, many_steps)
     assert np.array_equal(toks1, toksn[:toks1.size]), "thread count changed the CPU tokens"
-    return {"value": 1.0 / medn, "unit": "tokens/s", "cores": threads, "kind": "port",
+    return toksn, {"value": 1.0 / medn, "unit": "tokens/s", "cores": threads, "kind": "port",
             "nproc": nproc, "single_thread_value": 1.0 / med1,
             "median_step_ms": 1e3 * medn, "single_thread_median_step_ms": 1e3 * med1,
             "sample": (f"config-2 decode steps (B=1, V=262144) of oracle/orc.c -O2 -ffp-contract=off "
                        f"(RMSNorm, int4 matvec, softcap, repetition penalty, sample_token), timed per step "
                        f"inside C: median of {many_steps} steps at {threads} threads (nproc {nproc}, capped "
                        f"at {CPU_THREADS_CAP}) and of {one_steps} steps at 1 thread, each after one warm-up step")}
+
+
+def token_parity(gpu_toks, cpu_toks, W, S, B, g):
+    """The CPU baseline's config-2 tokens against the GPU line's on the same inputs (hidden row s,
+    Philox counter s, the same 256-id history growing by each step's token): the reference's
+    token-for-token gate (CONTRIBUTING.md:38-47). Up to the first difference both histories are
+    equal; a difference is reported with the oracle's CDF margin at that step (a near tie when
+    the margin is below 1e-3 of r), and the comparison stops there because the histories then
+    diverge."""
+    import orc_py as O
+    import synth
+    n = min(len(gpu_toks), len(cpu_toks))
+    diff = np.nonzero(np.asarray(gpu_toks[:n], np.uint32) != np.asarray(cpu_toks[:n], np.uint32))[0]
+    out = {"steps": n, "equal": n if diff.size == 0 else int(diff[0]), "near_ties": 0, "first_mismatch": None,
+           "kind": "oracle/orc.c decode steps vs the GPU line's first steps, identical inputs"}
+    if diff.size:
+        k = int(diff[0])
+        hist = np.concatenate([synth.uniform_ids(256, V, SEED), np.asarray(cpu_toks[:k], np.uint32)])
+        x = synth.hidden_states(1, D, SEED + 1, k)[0]
+        p = O.params(0.8, 0.95, 64, 1.1)
+        l = O.apply_modifiers(O.head_logits(W, S, B, g, x, threads=CPU_THREADS_CAP), p, 30.0, history=hist)
+        info = O.sample(l, p, O.philox_uniform(SEED, k))
+        margin = min(info.acc_at - info.r, info.r - info.acc_prev) / max(info.r, 1e-300)
+        out["first_mismatch"] = {"step": k, "gpu": int(gpu_toks[k]), "cpu": int(cpu_toks[k]), "cdf_margin_rel": margin}
+        out["near_ties"] = 1 if margin <= 1e-3 else 0
+    return out
 
 
 def main():
@@ -392,15 +419,18 @@ def main():
     log("generating the synthetic head")
     W, S, B, g = synth.make_head(V, D, SEED)
     if a.only == "cpu":
-        print(json.dumps({"only": a.only, **cpu_baseline(W, S, B, g)}), flush=True)
+        print(json.dumps({"only": a.only, **cpu_baseline(W, S, B, g)[1]}), flush=True)
         return
     head = T.LMHead(W, S, B, g, vocab=V, hidden=D)
     tsteps = max(1, a.timing_steps)
     total = a.warmup + a.steps + tsteps
     lines = {}
+    gpu_toks = None
     if a.only in (None, "b1"):
         log(f"B=1 sampled: warmup {a.warmup}, timed {a.steps}, head-timing pass {tsteps}")
-        main_line = measure(torch, head, SampledB1(T, torch, head, total), a.warmup, a.steps, tsteps)
+        b1 = SampledB1(T, torch, head, total)
+        main_line = measure(torch, head, b1, a.warmup, a.steps, tsteps)
+        gpu_toks = b1.tokens.cpu().numpy().astype(np.uint32)  # every step's token, step 0 first
     if a.only in (None, "greedy"):
         log("B=1 greedy")
         lines["greedy_b1"] = measure(torch, head, GreedyB1(T, torch, head, total), a.warmup, a.steps, tsteps)
@@ -460,7 +490,8 @@ def main():
         line["widened"] = widened_lines(T, torch)
     if not a.no_cpu:
         log("cpu baseline")
-        line["cpu_baseline"] = cpu_baseline(W, S, B, g)
+        cpu_toks, line["cpu_baseline"] = cpu_baseline(W, S, B, g)
+        line["parity"] = token_parity(gpu_toks, cpu_toks, W, S, B, g)
     print(json.dumps(line), flush=True)
 
 
