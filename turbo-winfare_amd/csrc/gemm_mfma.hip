@@ -393,19 +393,43 @@ __global__ __launch_bounds__(64 * WV, OCC) void k_head_mfma(
                         const uint32_t hb = mb ? hb1 : hb0;
                         if (hb == 0u) continue;
                         uint32_t cnt[16];
+                        if (full_tile && vec_ok) {
+                            // The lane's 16 rows of this half are four runs of four consecutive ids
+                            // (acc_row): a run with a bit set is read with one 16-byte load and
+                            // zeroed with one 16-byte store. Ids without a bit hold 0 already, and
+                            // no other lane touches these ids.
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const uint32_t rr = 32u * mb + acc_row(r, hl);
-                            cnt[r] = ((hb >> (rr & 31u)) & 1u) ? hrow[rr] : 0u;
+                            for (int q = 0; q < 4; ++q) {
+                                const uint32_t o = 32u * mb + 8u * (uint32_t)q + 4u * hl;
+                                uint4 c4 = make_uint4(0u, 0u, 0u, 0u);
+                                if ((hb >> (o & 31u)) & 15u) c4 = *reinterpret_cast<const uint4*>(hrow + o);
+                                cnt[4 * q] = c4.x;
+                                cnt[4 * q + 1] = c4.y;
+                                cnt[4 * q + 2] = c4.z;
+                                cnt[4 * q + 3] = c4.w;
+                            }
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) {
+                                const uint32_t o = 32u * mb + 8u * (uint32_t)q + 4u * hl;
+                                if ((hb >> (o & 31u)) & 15u)
+                                    *reinterpret_cast<uint4*>(hrow + o) = make_uint4(0u, 0u, 0u, 0u);
+                            }
+                        } else {
+#pragma unroll
+                            for (int r = 0; r < 16; ++r) {
+                                const uint32_t rr = 32u * mb + acc_row(r, hl);
+                                cnt[r] = ((hb >> (rr & 31u)) & 1u) ? hrow[rr] : 0u;
+                            }
+#pragma unroll
+                            for (int r = 0; r < 16; ++r)
+                                if (cnt[r]) hrow[32u * mb + acc_row(r, hl)] = 0u;
                         }
 #pragma unroll
                         for (int r = 0; r < 16; ++r)
-                            if (cnt[r]) {
-                                const uint32_t rr = 32u * mb + acc_row(r, hl);
-                                hrow[rr] = 0u;
-                                zz[16 * mb + r] = apply_entry(zz[16 * mb + r], ModEntry{base + rr, cnt[r], 0.0f, 0u}, row,
+                            if (cnt[r])
+                                zz[16 * mb + r] = apply_entry(zz[16 * mb + r],
+                                                              ModEntry{base + 32u * mb + acc_row(r, hl), cnt[r], 0.0f, 0u}, row,
                                                               ep.rep_limit);
-                            }
                     }
                 }
             }

@@ -1064,7 +1064,8 @@ __global__ __launch_bounds__(kMaxSelThreads) void k_fv_finish(SelectArgs a, uint
 // m - (j + 1) w up to rounding far below one bin, so m - (j + 2) w bounds the want-th largest
 // block maximum, and with it the want-th largest logit, from below (window_scan, one wave).
 // Needs |m| <= 1024 (value rounding << w) and the want-th maximum inside the window; the scan
-// returns 0 (not found) otherwise.
+// returns 0 (not found) otherwise. Every wave runs the scan on the same counts and so finds the
+// same bound, with no barrier between the scan and its use.
 constexpr uint32_t kWinBins = 256;
 constexpr float kWinWidth = 1.0f / 32.0f;
 template <uint32_t KP>
@@ -1077,27 +1078,23 @@ __device__ __attribute__((always_inline)) inline void window_add(SelShared& s, c
     }
 }
 __device__ inline uint32_t window_scan(SelShared& s, float m, uint32_t want) {
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    if (wave == 0u) {
-        const uint4 c = *reinterpret_cast<const uint4*>(&s.hu[4u * lane]);  // bins 4 lane .. 4 lane + 3
-        const uint32_t sum = c.x + c.y + c.z + c.w;
-        const uint32_t incl = wave_incl_scan(sum, lane);
-        const unsigned long long mk = __ballot(incl >= want);
-        uint32_t res = 0u;
-        if (mk != 0ull) {
-            const uint32_t L = (uint32_t)__ffsll((long long)mk) - 1u;
-            const uint32_t before = lane_read(incl - sum, (int)L);
-            const uint4 cl = *reinterpret_cast<const uint4*>(&s.hu[4u * L]);
-            uint32_t q = 3u;
-            if (before + cl.x >= want) q = 0u;
-            else if (before + cl.x + cl.y >= want) q = 1u;
-            else if (before + cl.x + cl.y + cl.z >= want) q = 2u;
-            res = float_key(m - (float)(4u * L + q + 2u) * kWinWidth);
-        }
-        if (lane == 0u) s.bu[6] = res;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint4 c = *reinterpret_cast<const uint4*>(&s.hu[4u * lane]);  // bins 4 lane .. 4 lane + 3
+    const uint32_t sum = c.x + c.y + c.z + c.w;
+    const uint32_t incl = wave_incl_scan(sum, lane);
+    const unsigned long long mk = __ballot(incl >= want);
+    uint32_t res = 0u;
+    if (mk != 0ull) {
+        const uint32_t L = (uint32_t)__ffsll((long long)mk) - 1u;
+        const uint32_t before = lane_read(incl - sum, (int)L);
+        const uint4 cl = *reinterpret_cast<const uint4*>(&s.hu[4u * L]);
+        uint32_t q = 3u;
+        if (before + cl.x >= want) q = 0u;
+        else if (before + cl.x + cl.y >= want) q = 1u;
+        else if (before + cl.x + cl.y + cl.z >= want) q = 2u;
+        res = float_key(m - (float)(4u * L + q + 2u) * kWinWidth);
     }
-    __syncthreads();
-    return s.bu[6];
+    return __builtin_amdgcn_readfirstlane(res);
 }
 
 // ---- the kernel ----------------------------------------------------------------------------------
@@ -1272,6 +1269,8 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
             uint32_t tau = 0u;
             if (win && fabsf(m) <= 1024.0f) tau = window_scan(s, m, want);
             if (a.ntile > want && tau == 0u) {
+                // the window's counts may still be read by a slower wave's scan
+                __syncthreads();
                 constexpr float kTauSpan = 32.0f;
                 constexpr float kTauInv = (float)kBins / kTauSpan;
                 bool found = false;
