@@ -144,6 +144,48 @@ def test_step_normed_large_activations(small_head):
         assert U.draw_check(want, O.params(0.0), 0.0, int(toks[b]), mode="margin") in ("exact", "within")
 
 
+@pytest.mark.parametrize("vocab", [4099, 4100])
+@pytest.mark.parametrize("batch", [5, 40, 100])
+def test_mfma_history_modifiers_partial_tiles(vocab, batch):
+    """Repetition, presence and frequency penalties in the matrix-core epilogue at 32, 64 and 128
+    columns per workgroup, where the history counts are read and cleared as 16-byte runs on full
+    tiles and one id at a time on a partial last tile (4100 ids: 4 in the last tile) or when rows
+    are not 16-byte aligned (4099 ids). The step's final logits must equal the oracle's modifiers
+    applied to the head's raw logits bit for bit, twice in a row with different histories (the
+    first step's counts must all be cleared)."""
+    W, S, B, g = synth.make_head(vocab, D, 107)
+    h = T.LMHead(W, S, B, g, vocab=vocab, hidden=D)
+    try:
+        x = synth.hidden_states(batch, D, 14)
+        xd = dev(x)
+        rows = [T.row_default(temperature=0.8, top_k=40, top_p=0.9, repetition_penalty=1.3, presence_penalty=0.4,
+                              frequency_penalty=0.2, seed=60 + b, counter=1) for b in range(batch)]
+        xn = torch.empty((batch, D), dtype=torch.float32, device="cuda")
+        h.rms_norm(xd, batch, xn)
+        raw = torch.empty((batch, vocab), dtype=torch.float32, device="cuda")
+        h.logits(xn, batch, raw)
+        h.sync()
+        raw = raw.cpu().numpy()
+        for call in range(2):
+            n = 300
+            hists = np.stack([synth.zipf_ids(n, vocab, 1.1, 900 + 31 * call + b) for b in range(batch)]).astype(np.uint32)
+            hists[:, :6] = [vocab - 1, vocab - 2, vocab - 4, vocab - 1, vocab + 3, 0]  # the last tile, repeats, ignored ids
+            hd = dev(hists.view(np.int32))
+            hl = torch.full((batch,), n, dtype=torch.int32, device="cuda")
+            inp, keep = h.make_inputs(batch, rows, hidden=xd, history=hd, history_len=hl)
+            tok = torch.zeros(batch, dtype=torch.int32, device="cuda")
+            got = torch.empty((batch, vocab), dtype=torch.float32, device="cuda")
+            h.step(inp, tok, got)
+            h.sync()
+            got = got.cpu().numpy()
+            for b in sorted({0, batch // 2, batch - 1}):
+                want = O.apply_modifiers(raw[b], O.params(0.8, 0.9, 40, 1.3, 0.4, 0.2), 30.0, history=hists[b])
+                bad = np.nonzero(got[b].view(np.uint32) != want.view(np.uint32))[0]
+                assert bad.size == 0, (call, b, [(int(i), float(got[b, i]), float(want[i])) for i in bad[:6]])
+    finally:
+        h.close()
+
+
 @pytest.mark.parametrize("vocab,batch", [(300, 40), (4099, 48), (1100, 33)])
 def test_logits_mfma_partial_workgroups(vocab, batch):
     """64-column heads run 16 tiles per workgroup: vocabularies of 5, 65 and 18 tiles leave the
