@@ -114,3 +114,15 @@ def test_null_handle_errors():
     assert lib.turbo_lmhead_synchronize(None) == 0
     assert "handle" in T.last_error()
     lib.turbo_lmhead_destroy(None)  # no-op
+
+
+def test_reference_rng_position_must_fit_an_int():
+    """TURBO_RNG_REFERENCE maps counter to the reference's int position (src/sampling.cpp:63):
+    negative positions as 64-bit two's complement are accepted, values outside int are rejected."""
+    ok = lambda c: T.validate(T.row_default(rng=T.TURBO_RNG_REFERENCE, counter=c))  # noqa: E731
+    assert ok(0)[0] and ok(2**31 - 1)[0] and ok(2**64 - 1)[0] and ok(2**64 - 2**31)[0]
+    for c in (2**31, 2**40, 2**64 - 2**31 - 1):
+        good, why = ok(c)
+        assert not good and "int position" in why, c
+    # Philox counters are unrestricted
+    assert T.validate(T.row_default(counter=2**63 + 5))[0]

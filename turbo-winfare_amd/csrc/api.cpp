@@ -8,6 +8,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <memory>
@@ -137,6 +138,15 @@ bool validate_row(const TurboSamplingRow& p, std::string* why) {
     if (p.rng != TURBO_RNG_PHILOX && p.rng != TURBO_RNG_REFERENCE) {
         *why = "rng must be TURBO_RNG_PHILOX or TURBO_RNG_REFERENCE";
         return false;
+    }
+    // the reference's position is an int (src/sampling.cpp:63): counter holds it as a 64-bit
+    // two's-complement value, which must fit
+    if (p.rng == TURBO_RNG_REFERENCE) {
+        const int64_t pos = static_cast<int64_t>(p.counter);
+        if (pos < INT32_MIN || pos > INT32_MAX) {
+            *why = "counter must hold an int position (-2^31 .. 2^31-1) for TURBO_RNG_REFERENCE";
+            return false;
+        }
     }
     if ((p.flags & ~static_cast<uint32_t>(TURBO_ROW_FULL_VOCAB)) != 0u) {
         *why = "unknown row flags";
@@ -329,6 +339,9 @@ void check_head_path(const Head& h, int B) {
     if (B > 2 && !h.mfma_ok)
         throw std::runtime_error("this head's scales or biases exceed the fp16 range (|x| > 65504), which the "
                                  "matrix-core path for batches above 2 rows cannot represent; call with batch <= 2");
+    if (B > 2 && !tdt::mfma_table_fits(h))
+        throw std::runtime_error("this head's table exceeds the 4 GiB the matrix-core path for batches above 2 "
+                                 "rows addresses; call with batch <= 2");
 }
 
 // The head over normalised rows x with greedy row parameters (turbo_lmhead_logits,
@@ -587,7 +600,7 @@ TURBO_DT_API void* turbo_lmhead_create(const TurboLMHeadDesc* d) {
         int ndev = 0;
         check_hip(hipGetDeviceCount(&ndev), "hipGetDeviceCount");
         if (d->device < 0 || d->device >= ndev) throw std::runtime_error("no such HIP device");
-        check_hip(hipSetDevice(d->device), "hipSetDevice");
+        tdt::DeviceGuard dg(d->device);
         h.device = d->device;
         h.V = d->vocab_size;
         h.D = d->hidden_size;
@@ -696,7 +709,7 @@ TURBO_DT_API void turbo_lmhead_destroy(void* handle) {
     if (!handle) return;
     try {
         HandleBox* b = box(handle);
-        (void)hipSetDevice(b->h.device);
+        tdt::DeviceGuard dg(b->h.device);
         free_head(b->h);
         b->magic = 0;
         delete b;
@@ -716,7 +729,7 @@ TURBO_DT_API int turbo_lmhead_synchronize(void* handle) {
     clear_error();
     API_TRY
     Head& h = box(handle)->h;
-    check_hip(hipSetDevice(h.device), "hipSetDevice");
+    tdt::DeviceGuard dg(h.device);
     check_hip(hipStreamSynchronize(h.stream), "synchronize");
     if (h.overflow_host && *h.overflow_host) {
         const uint32_t row = *h.overflow_host - 1u;
@@ -781,7 +794,7 @@ TURBO_DT_API int turbo_lmhead_step(void* handle, const TurboStepInputs* in,
     clear_error();
     API_TRY
     HandleBox* bx = box(handle);
-    check_hip(hipSetDevice(bx->h.device), "hipSetDevice");
+    tdt::DeviceGuard dg(bx->h.device);
     if (!in || !in->hidden) throw std::runtime_error("hidden is NULL");
     return run_rows(bx->h, bx, in, out, in->hidden, nullptr);
     API_CATCH(0)
@@ -792,7 +805,7 @@ TURBO_DT_API int turbo_sample_logits(void* handle, float* logits, const TurboSte
     clear_error();
     API_TRY
     HandleBox* bx = box(handle);
-    check_hip(hipSetDevice(bx->h.device), "hipSetDevice");
+    tdt::DeviceGuard dg(bx->h.device);
     if (!logits) throw std::runtime_error("logits is NULL");
     return run_rows(bx->h, bx, in, out, nullptr, logits);
     API_CATCH(0)
@@ -802,7 +815,7 @@ TURBO_DT_API int turbo_lmhead_rms_norm(void* handle, const float* x, int batch, 
     clear_error();
     API_TRY
     Head& h = box(handle)->h;
-    check_hip(hipSetDevice(h.device), "hipSetDevice");
+    tdt::DeviceGuard dg(h.device);
     check_batch(h, batch);
     if (!x || !out) throw std::runtime_error("x or out is NULL");
     tdt::DevRow rows[kMaxBatch];
@@ -818,7 +831,7 @@ TURBO_DT_API int turbo_lmhead_logits(void* handle, const void* x, int x_dtype, i
     API_TRY
     HandleBox* bx = box(handle);
     Head& h = bx->h;
-    check_hip(hipSetDevice(h.device), "hipSetDevice");
+    tdt::DeviceGuard dg(h.device);
     check_batch(h, batch);
     if (!x || !logits) throw std::runtime_error("x or logits is NULL");
     if (x_dtype != TURBO_HIDDEN_F32 && x_dtype != TURBO_HIDDEN_BF16)
@@ -836,7 +849,7 @@ TURBO_DT_API int turbo_lmhead_greedy(void* handle, const void* x, int x_dtype, i
     API_TRY
     HandleBox* bx = box(handle);
     Head& h = bx->h;
-    check_hip(hipSetDevice(h.device), "hipSetDevice");
+    tdt::DeviceGuard dg(h.device);
     check_batch(h, batch);
     if (!x || !tokens) throw std::runtime_error("x or tokens is NULL");
     if (x_dtype != TURBO_HIDDEN_F32 && x_dtype != TURBO_HIDDEN_BF16)
@@ -881,7 +894,7 @@ TURBO_DT_API int turbo_lmhead_enable_head_timing(void* handle, int enable) {
     API_TRY
     HandleBox* bx = box(handle);
     Head& h = bx->h;
-    check_hip(hipSetDevice(h.device), "hipSetDevice");
+    tdt::DeviceGuard dg(h.device);
     if (enable && !h.t_start[0]) {
         for (int i = 0; i < Head::kTimerSlots; ++i) {
             check_hip(hipEventCreate(&h.t_start[i]), "timer events");
@@ -902,7 +915,7 @@ TURBO_DT_API int turbo_lmhead_head_kernel_time(void* handle, double* total_ms, i
     API_TRY
     HandleBox* bx = box(handle);
     Head& h = bx->h;
-    check_hip(hipSetDevice(h.device), "hipSetDevice");
+    tdt::DeviceGuard dg(h.device);
     check_hip(hipStreamSynchronize(h.stream), "timer sync");
     double ms = bx->t_accum_ms;
     int n = bx->t_accum_n;
@@ -933,7 +946,7 @@ TURBO_DT_API int turbo_lmhead_embed(void* handle, const uint32_t* tokens, int n,
     API_TRY
     HandleBox* bx = box(handle);
     Head& h = bx->h;
-    check_hip(hipSetDevice(h.device), "hipSetDevice");
+    tdt::DeviceGuard dg(h.device);
     if (n < 0) throw std::runtime_error("n must be >= 0");
     if (n > 0 && (!tokens || !out)) throw std::runtime_error("tokens or out is NULL");
     if (n > 65535 * 16) throw std::runtime_error("at most 1048560 tokens per call");

@@ -229,6 +229,12 @@ void launch_head_digits(const Head& h, int batch, const EpiArgs& ep, hipStream_t
                         hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
 void launch_head_mfma(const Head& h, int batch, const EpiArgs& ep, hipStream_t st,
                       hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
+// The matrix-core head addresses the tiled table through buffer resources, whose sizes and
+// offsets are 32-bit: it serves tables of at most 4 GiB.
+inline bool mfma_table_fits(const Head& h) {
+    return (uint64_t)h.ntile * h.NC * kTileRows * 16u <= 0xFFFFFFFFull &&
+           (uint64_t)h.ntile * h.G * kTileRows * 4u <= 0xFFFFFFFFull;
+}
 // epilogue over caller logits (no GEMV): logits are read, modified and summarised in place.
 void launch_logits_epilogue(const Head& h, int batch, const EpiArgs& ep, hipStream_t st);
 
@@ -272,6 +278,22 @@ void launch_embed(const Head& h, const uint32_t* tokens, int n, float* out, floa
 
 // Throws std::runtime_error with the HIP error string on failure.
 void check_hip(hipError_t e, const char* what);
+
+// Makes `dev` the current device for the guard's lifetime and then restores the caller's, so an
+// entry point leaves the calling thread's current device as it found it.
+struct DeviceGuard {
+    int prev = -1;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) check_hip(hipSetDevice(dev), "hipSetDevice");
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+    DeviceGuard(const DeviceGuard&) = delete;
+    DeviceGuard& operator=(const DeviceGuard&) = delete;
+};
 
 // api.cpp: turbo_sample_logits on a head whose scratch the caller provides (h.Wt may be null: no
 // head kernel runs). Validates the rows and enqueues the modifier epilogue and the select on

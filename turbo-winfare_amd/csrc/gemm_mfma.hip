@@ -546,6 +546,7 @@ void launch_head_mfma(const Head& h, int batch, const EpiArgs& ep, hipStream_t s
                       hipEvent_t ev1) {
     const uint32_t B = (uint32_t)batch;
     if (B > 256u) throw std::runtime_error("MFMA head supports batch <= 256");
+    if (!mfma_table_fits(h)) throw std::runtime_error("MFMA head supports tables of at most 4 GiB");
     const int nb = (B <= 32u) ? 1 : (B <= 64u) ? 2 : 4;
     const uint32_t ncol = 32u * (uint32_t)nb;
     const uint32_t wv = (nb == 2) ? 16u : 4u;  // waves (tiles) per workgroup, as instantiated below

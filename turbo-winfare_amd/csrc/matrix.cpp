@@ -76,7 +76,7 @@ TURBO_DT_API void* turbo_int4_matrix_create(uint32_t rows, uint32_t in_dim, int 
     int ndev = 0;
     tdt::check_hip(hipGetDeviceCount(&ndev), "hipGetDeviceCount");
     if (device < 0 || device >= ndev) throw std::runtime_error("no such HIP device");
-    tdt::check_hip(hipSetDevice(device), "hipSetDevice");
+    tdt::DeviceGuard dg(device);
     auto* m = new MatrixBox;
     m->device = device;
     m->rows = rows;
@@ -103,7 +103,7 @@ TURBO_DT_API int turbo_int4_matrix_load(void* handle, const uint8_t* weight, con
     MAT_TRY
     MatrixBox* m = mbox(handle);
     if (!weight || !scales || !biases) throw std::runtime_error("weight/scales/biases are NULL");
-    tdt::check_hip(hipSetDevice(m->device), "hipSetDevice");
+    tdt::DeviceGuard dg(m->device);
     hipStream_t st = static_cast<hipStream_t>(hip_stream);
     m->note(st);
     const size_t wbytes = (size_t)m->rows * (m->D / 2u), gcount = (size_t)m->rows * m->G;
@@ -141,7 +141,7 @@ TURBO_DT_API void turbo_int4_matrix_destroy(void* handle) {
     if (!handle) return;
     try {
         MatrixBox* m = mbox(handle);
-        (void)hipSetDevice(m->device);
+        tdt::DeviceGuard dg(m->device);
         if (m->many) {
             (void)hipDeviceSynchronize();
         } else {
@@ -187,7 +187,7 @@ TURBO_DT_API int turbo_int4_matvec_grouped(void* const* matrices, int count, con
         tiles += m->ntile;
     }
     a.count = static_cast<uint32_t>(count);
-    tdt::check_hip(hipSetDevice(device), "hipSetDevice");
+    tdt::DeviceGuard dg(device);
     tdt::launch_matvec_grouped(a, tiles, static_cast<hipStream_t>(hip_stream));
     return 1;
     MAT_CATCH(0)
