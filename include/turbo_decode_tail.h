@@ -176,7 +176,8 @@ typedef struct {
     int rng;                    /* TURBO_RNG_* */
     int has_seed;               /* TURBO_RNG_REFERENCE only */
     uint64_t seed;
-    uint64_t counter;           /* Philox counter (decode step), or the reference position */
+    uint64_t counter;           /* Philox counter (decode step), or the reference's int position
+                                   (two's complement; must fit in int for TURBO_RNG_REFERENCE) */
     uint32_t flags;             /* TURBO_ROW_* */
 } TurboSamplingRow;
 
