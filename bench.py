@@ -463,7 +463,7 @@ def main():
             measured = {}
     traffic = measured.get("b1")
     for name, ln in lines.items():
-        ln["roofline"]["traffic"] = measured.get(name)
+        ln["roofline"]["traffic"] = measured.get({"greedy_b1": "greedy"}.get(name, name))
     roof = dict(main_line["roofline"])
     roof["traffic"] = traffic
     line = {
