@@ -186,6 +186,65 @@ def test_mfma_history_modifiers_partial_tiles(vocab, batch):
         h.close()
 
 
+@pytest.mark.parametrize("batch", [1, 2, 5, 40, 100])
+def test_step_all_modifiers_partial_last_tile(batch):
+    """The whole step with every modifier (logit bias with duplicate ids, repetition, presence,
+    frequency and a ban mask) on a vocabulary whose last 64-id tile holds 3 ids (4099), through
+    each head kernel: the folded digit kernel (1 and 2 rows) and the matrix-core kernels at 32, 64
+    and 128 columns. Bias, history and ban hit the last tile's ids. The final logits must equal
+    the oracle's modifiers on the head's raw logits bit for bit, and the tokens must pass the
+    interval check on those logits. Rows past the vocabulary stay -inf-free: the returned logits
+    hold exactly vocab ids per row."""
+    vocab = 4099
+    W, S, B, g = synth.make_head(vocab, D, 109)
+    h = T.LMHead(W, S, B, g, vocab=vocab, hidden=D)
+    try:
+        x = synth.hidden_states(batch, D, 15)
+        xd = dev(x)
+        cfgs = [(0.9, 0.9, 40), (0.7, 0.95, 0), (1.2, 0.8, 100)]
+        rows = [T.row_default(temperature=cfgs[b % 3][0], top_p=cfgs[b % 3][1], top_k=cfgs[b % 3][2] or 64,
+                              repetition_penalty=1.25, presence_penalty=0.3, frequency_penalty=0.15,
+                              seed=70 + b, counter=2) for b in range(batch)]
+        nh, nbias = 400, 120
+        hists = np.stack([synth.zipf_ids(nh, vocab, 1.1, 950 + b) for b in range(batch)]).astype(np.uint32)
+        hists[:, :4] = [vocab - 1, vocab - 3, vocab - 1, vocab + 9]
+        bl = [synth.bias_list(nbias, vocab, -3.0, 3.0, 960, b) for b in range(batch)]
+        bids = np.stack([a for a, _ in bl]).astype(np.uint32)
+        bids[:, :3] = [vocab - 2, vocab - 2, vocab - 1]      # the last tile, a duplicate
+        bvals = np.stack([v for _, v in bl])
+        bans = np.stack([synth.ban_mask(vocab, 0.05, 970, b) for b in range(batch)])
+        bans[:, -1] |= np.uint32(1 << ((vocab - 3) % 32))    # a banned id in the last tile
+        kw = dict(history=dev(hists.view(np.int32)), history_len=torch.full((batch,), nh, dtype=torch.int32, device="cuda"),
+                  ban=dev(bans.view(np.int32)), bias_ids=dev(bids.view(np.int32)), bias_values=dev(bvals),
+                  bias_count=torch.full((batch,), nbias, dtype=torch.int32, device="cuda"))
+        inp, keep = h.make_inputs(batch, rows, hidden=xd, **kw)
+        tok = torch.zeros(batch, dtype=torch.int32, device="cuda")
+        got = torch.full((batch, vocab + 1), 7.0, dtype=torch.float32, device="cuda")
+        h.step(inp, tok, got)
+        xn = torch.empty((batch, D), dtype=torch.float32, device="cuda")
+        h.rms_norm(xd, batch, xn)
+        raw = torch.empty((batch, vocab), dtype=torch.float32, device="cuda")
+        h.logits(xn, batch, raw)
+        h.sync()
+        got, raw, toks = got.cpu().numpy(), raw.cpu().numpy(), tok.cpu().numpy()
+        flat = got.reshape(-1)[:batch * vocab].reshape(batch, vocab)  # the step writes [batch][vocab]
+        assert np.all(got.reshape(-1)[batch * vocab:] == 7.0)          # nothing past it
+        ps, us, finals = [], [], []
+        for b in range(batch):
+            p = O.params(rows[b].temperature, rows[b].top_p, rows[b].top_k, 1.25, 0.3, 0.15)
+            want = O.apply_modifiers(raw[b], p, 30.0, history=hists[b], bias_ids=bids[b], bias_values=bvals[b],
+                                     ban=bans[b])
+            bad = np.nonzero(flat[b].view(np.uint32) != want.view(np.uint32))[0]
+            assert bad.size == 0, (b, [(int(i), float(flat[b, i]), float(want[i])) for i in bad[:6]])
+            assert np.isneginf(flat[b, vocab - 3])
+            ps.append(p)
+            us.append(T.row_uniform(rows[b]))
+            finals.append(want)
+        U.check_tokens(ps, toks.astype(np.uint32), finals, us, label=f"all modifiers B={batch}")
+    finally:
+        h.close()
+
+
 @pytest.mark.parametrize("vocab,batch", [(300, 40), (4099, 48), (1100, 33)])
 def test_logits_mfma_partial_workgroups(vocab, batch):
     """64-column heads run 16 tiles per workgroup: vocabularies of 5, 65 and 18 tiles leave the
