@@ -397,8 +397,8 @@ def token_parity(gpu_toks, cpu_toks, W, S, B, g):
 def main():
     a = parse()
     if a.gpus != 1:
-        print(f"bench.py measures one GPU only (got --gpus {a.gpus}); the sharded design is in DESIGN.md",
-              file=sys.stderr)
+        print(f"bench.py measures one GPU only (got --gpus {a.gpus}): the head would shard by vocabulary "
+              f"rows across GPUs, which is not implemented", file=sys.stderr)
         sys.exit(2)
     import torch
     if a.copy_calibration:

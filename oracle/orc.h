@@ -157,7 +157,7 @@ void orc_apply_presence_frequency(float* logits, uint32_t vocab, const uint32_t*
 /* Banned tokens: bit (id % 32) of words[id / 32] set -> logit = -inf. */
 void orc_apply_ban(float* logits, uint32_t vocab, const uint32_t* words);
 
-/* The whole per-row modifier chain in the order this build fixes:
+/* The whole per-row modifier chain in the order the library applies it:
  *   bias -> repetition penalty (reference rule, after softcap) -> presence/frequency -> ban.
  * Any pointer may be NULL / count 0 to skip that stage. */
 void orc_apply_modifiers(float* logits, uint32_t vocab, const orc_params* p, float softcap,
