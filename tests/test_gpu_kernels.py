@@ -245,6 +245,39 @@ def test_step_all_modifiers_partial_last_tile(batch):
         h.close()
 
 
+@pytest.mark.parametrize("batch", [1, 2, 4])
+def test_step_injected_uniforms(small_head, batch):
+    """Caller-supplied uniforms (TurboStepInputs.uniforms) replace each row's generator: the
+    edge values 0 (the top survivor) and 1 - 2^-24 (the last one) and two inner values, on
+    shortlist and full-vocabulary rows, through the folded digit head (1, 2 rows) and the
+    matrix-core head (4 rows). The report carries the uniform used, and every token is the oracle
+    sampler's on the GPU's logits with that uniform (interval-checked)."""
+    h, (W, S, B, g) = small_head
+    cfgs = [(0.8, 0.95, 64, 0), (1.0, 0.9, 0, 1), (0.7, 1.0, 40, 0), (1.3, 0.5, 0, 1)]
+    us_all = np.array([0.0, 1.0 - 2.0 ** -24, 0.5, 0.123456], np.float32)
+    x = synth.hidden_states(batch, D, 16)
+    xd = dev(x)
+    for shift in range(4):
+        rows = [T.row_default(temperature=cfgs[(b + shift) % 4][0], top_p=cfgs[(b + shift) % 4][1],
+                              top_k=cfgs[(b + shift) % 4][2], seed=5, counter=9,
+                              flags=T.TURBO_ROW_FULL_VOCAB if cfgs[(b + shift) % 4][3] else 0)
+                for b in range(batch)]
+        us = np.roll(us_all, shift)[:batch].copy()
+        ud = dev(us)
+        inp, keep = h.make_inputs(batch, rows, hidden=xd, uniforms=ud)
+        tok = torch.zeros(batch, dtype=torch.int32, device="cuda")
+        lg = torch.empty((batch, V_SMALL), dtype=torch.float32, device="cuda")
+        rep = torch.zeros((batch, 56 // 4), dtype=torch.int32, device="cuda")
+        h.step(inp, tok, lg, rep)
+        h.sync()
+        got = rep.cpu().numpy()
+        assert np.array_equal(got[:, 1].view(np.float32), us), (shift, got[:, 1].view(np.float32), us)
+        ps = [O.params(r.temperature, r.top_p, r.top_k, 1.0, 0.0, 0.0, r.flags) for r in rows]
+        c = U.check_tokens(ps, tok.cpu().numpy().astype(np.uint32), lg.cpu().numpy(), [float(u) for u in us],
+                           within_frac=1.0, label=f"injected uniforms B={batch} shift {shift}")
+        assert c["exact"] == batch
+
+
 @pytest.mark.parametrize("vocab,batch", [(300, 40), (4099, 48), (1100, 33)])
 def test_logits_mfma_partial_workgroups(vocab, batch):
     """64-column heads run 16 tiles per workgroup: vocabularies of 5, 65 and 18 tiles leave the
