@@ -138,7 +138,9 @@ TURBO_DT_API void* turbo_lmhead_create(const TurboLMHeadDesc* desc);
  * other streams are not waited for) and frees everything (src/runner.cpp:25-42). NULL is a
  * no-op. */
 TURBO_DT_API void turbo_lmhead_destroy(void* handle);
-/* hip_stream is a hipStream_t (NULL = the null stream). Must be created at default priority. */
+/* hip_stream is a hipStream_t (NULL = the null stream). Must be created at default priority.
+ * Switching to another stream first waits for the current one, whose steps may still be using
+ * the handle's scratch buffers. */
 TURBO_DT_API int turbo_lmhead_set_stream(void* handle, void* hip_stream);
 /* Waits for the handle's stream. Returns 0 (once) when a step since the last call found a full
  * history under TURBO_STEP_APPEND_HISTORY (TURBO_STATUS_HISTORY_FULL). */

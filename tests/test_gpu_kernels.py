@@ -278,6 +278,66 @@ def test_step_injected_uniforms(small_head, batch):
         assert c["exact"] == batch
 
 
+@pytest.mark.parametrize("batch", [1, 4])
+def test_step_on_caller_stream_and_head_timing(batch):
+    """turbo_lmhead_set_stream: steps enqueued on a caller's stream run after the work already on
+    it (here a hidden-state copy queued behind a chain of matrix products) and give the null
+    stream's tokens, logits and reports bit for bit. turbo_lmhead_enable_head_timing counts every
+    N-th head launch: 3 of 3 at N = 1, launches 0, 3 and 6 of 7 at N = 3, none when off."""
+    W, S, B, g = synth.make_head(V_SMALL, D, 101)
+    h = T.LMHead(W, S, B, g, vocab=V_SMALL, hidden=D)
+    try:
+        rows = [T.row_default(temperature=0.8, top_p=0.95, top_k=64, seed=3 + b, counter=1) for b in range(batch)]
+        x = synth.hidden_states(batch, D, 21)
+        xd = dev(x)
+
+        def outputs():
+            return (torch.zeros(batch, dtype=torch.int32, device="cuda"),
+                    torch.empty((batch, V_SMALL), dtype=torch.float32, device="cuda"),
+                    torch.zeros((batch, 56 // 4), dtype=torch.int32, device="cuda"))
+
+        tok0, lg0, rep0 = outputs()
+        inp0, keep0 = h.make_inputs(batch, rows, hidden=xd)
+        h.step(inp0, tok0, lg0, rep0)
+        h.sync()
+
+        s = torch.cuda.Stream()
+        xs = torch.zeros_like(xd)
+        tok1, lg1, rep1 = outputs()
+        torch.cuda.synchronize()
+        h.set_stream(s.cuda_stream)
+        h.enable_head_timing(True, every=1)
+        with torch.cuda.stream(s):
+            m = torch.full((2048, 2048), 1.0 / 2048, device="cuda")
+            for _ in range(8):
+                m = m @ m
+            xs.copy_(xd)
+        inp1, keep1 = h.make_inputs(batch, rows, hidden=xs)
+        for _ in range(3):
+            h.step(inp1, tok1, lg1, rep1)
+        h.sync()
+        ms, n = h.head_kernel_time(reset=True)
+        assert n == 3 and ms > 0.0, (ms, n)
+        assert np.array_equal(tok1.cpu().numpy(), tok0.cpu().numpy())
+        assert np.array_equal(lg1.cpu().numpy().view(np.uint32), lg0.cpu().numpy().view(np.uint32))
+        assert np.array_equal(rep1.cpu().numpy(), rep0.cpu().numpy())
+
+        h.enable_head_timing(True, every=3)
+        for _ in range(7):
+            h.step(inp1, tok1, lg1, rep1)
+        ms, n = h.head_kernel_time(reset=True)
+        assert n == 3 and ms > 0.0, (ms, n)
+        h.enable_head_timing(False)
+        for _ in range(2):
+            h.step(inp1, tok1, lg1, rep1)
+        ms, n = h.head_kernel_time(reset=True)
+        assert n == 0 and ms == 0.0, (ms, n)
+        h.set_stream(None)  # waits for s
+        assert np.array_equal(tok1.cpu().numpy(), tok0.cpu().numpy())
+    finally:
+        h.close()
+
+
 @pytest.mark.parametrize("vocab,batch", [(300, 40), (4099, 48), (1100, 33)])
 def test_logits_mfma_partial_workgroups(vocab, batch):
     """64-column heads run 16 tiles per workgroup: vocabularies of 5, 65 and 18 tiles leave the

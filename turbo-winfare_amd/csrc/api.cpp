@@ -720,7 +720,15 @@ TURBO_DT_API void turbo_lmhead_destroy(void* handle) {
 TURBO_DT_API int turbo_lmhead_set_stream(void* handle, void* stream) {
     clear_error();
     API_TRY
-    box(handle)->h.stream = static_cast<hipStream_t>(stream);
+    Head& h = box(handle)->h;
+    const hipStream_t next = static_cast<hipStream_t>(stream);
+    if (next != h.stream) {
+        // the handle's scratch and timer events belong to work already on the old stream: let it
+        // finish before the next step can reuse them from another stream
+        tdt::DeviceGuard dg(h.device);
+        check_hip(hipStreamSynchronize(h.stream), "set_stream: wait for the previous stream");
+        h.stream = next;
+    }
     return 1;
     API_CATCH(0)
 }
@@ -894,6 +902,7 @@ TURBO_DT_API int turbo_lmhead_enable_head_timing(void* handle, int enable) {
     API_TRY
     HandleBox* bx = box(handle);
     Head& h = bx->h;
+    if (enable < 0) throw std::runtime_error("enable must be >= 0");
     tdt::DeviceGuard dg(h.device);
     if (enable && !h.t_start[0]) {
         for (int i = 0; i < Head::kTimerSlots; ++i) {
@@ -901,7 +910,6 @@ TURBO_DT_API int turbo_lmhead_enable_head_timing(void* handle, int enable) {
             check_hip(hipEventCreate(&h.t_stop[i]), "timer events");
         }
     }
-    if (enable < 0) throw std::runtime_error("enable must be >= 0");
     h.timing = enable != 0;
     h.t_stride = enable > 1 ? static_cast<uint32_t>(enable) : 1u;
     h.t_launch = 0;

@@ -323,6 +323,10 @@ class LMHead:
     def sync(self) -> None:
         _ok(self.lib.turbo_lmhead_synchronize(self.h))
 
+    def set_stream(self, stream) -> None:
+        """stream: a hipStream_t as an int (torch.cuda.Stream.cuda_stream) or None for the null stream."""
+        _ok(self.lib.turbo_lmhead_set_stream(self.h, stream))
+
     def limits(self) -> tuple[int, int]:
         mb, mm = C.c_int(), C.c_int()
         _ok(self.lib.turbo_lmhead_limits(self.h, C.byref(mb), C.byref(mm)))
