@@ -253,19 +253,45 @@ __device__ __attribute__((always_inline)) inline void rank_top(SelShared& s, uin
     __syncthreads();
 }
 
-// Visits every (value, index) of a row with kInflight independent loads per thread in flight.
+// A row pass reads float4s when the row allows it (length a multiple of 4, 16-byte aligned).
+__device__ inline bool row_vec(const float* l, uint32_t V) { return (V & 3u) == 0u && ((uintptr_t)l & 15u) == 0u; }
+
+// The first round of a row pass's loads, issued ahead of work the pass does not depend on (the
+// row parameters) so that their latency overlaps it. Holds nothing for a row that takes the
+// scalar pass.
+struct RowPre {
+    float4 q[kInflight];
+};
+__device__ inline void row_preload(const float* l, uint32_t V, RowPre& p) {
+    if (!row_vec(l, V)) return;
+    const float4* l4 = reinterpret_cast<const float4*>(l);
+    const uint32_t V4 = V >> 2;
+#pragma unroll
+    for (int j = 0; j < kInflight; ++j) {
+        const uint32_t idx = (uint32_t)j * sel_nt() + threadIdx.x;
+        p.q[j] = (idx < V4) ? l4[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
+// Visits every (value, index) of a row with kInflight independent loads per thread in flight;
+// the first round comes from pre when given (row_preload of the same l and V).
 template <class F>
-__device__ inline void row_pass(const float* l, uint32_t V, F&& f) {
+__device__ inline void row_pass(const float* l, uint32_t V, F&& f, const RowPre* pre = nullptr) {
     const uint32_t tid = threadIdx.x;
-    if ((V & 3u) == 0u && ((uintptr_t)l & 15u) == 0u) {
+    if (row_vec(l, V)) {
         const float4* l4 = reinterpret_cast<const float4*>(l);
         const uint32_t V4 = V >> 2;
         for (uint32_t base = 0; base < V4; base += kInflight * sel_nt()) {
             float4 q[kInflight];
+            if (pre && base == 0u) {
 #pragma unroll
-            for (int j = 0; j < kInflight; ++j) {
-                const uint32_t idx = base + (uint32_t)j * sel_nt() + tid;
-                q[j] = (idx < V4) ? l4[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+                for (int j = 0; j < kInflight; ++j) q[j] = pre->q[j];
+            } else {
+#pragma unroll
+                for (int j = 0; j < kInflight; ++j) {
+                    const uint32_t idx = base + (uint32_t)j * sel_nt() + tid;
+                    q[j] = (idx < V4) ? l4[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
             }
 #pragma unroll
             for (int j = 0; j < kInflight; ++j) {
@@ -455,16 +481,20 @@ __device__ __attribute__((always_inline)) inline int find_cross(SelShared& s, co
 
 // One wave's lane sums of a kVBins histogram (lane l: bins 32 l .. 32 l + 31, exact integers)
 // and their inclusive and exclusive prefixes, for several crossing searches over one histogram.
+// Lane l adds its 32 bins starting at bin (l mod 32) of its range: read in bin order, the lanes'
+// 256-byte-apart addresses would all fall in one LDS bank on every read. Integer sums do not
+// depend on the order.
 struct WaveHist {
     unsigned long long loc, incl, run;
 };
 __device__ __attribute__((always_inline)) inline WaveHist wave_hist(const unsigned long long* h) {
     constexpr uint32_t kPer = kVBins / 64u;
+    static_assert((kPer & (kPer - 1u)) == 0u, "the rotated read needs a power-of-two range per lane");
     const uint32_t lane = threadIdx.x & 63u, b0 = lane * kPer;
     WaveHist w;
     w.loc = 0ull;
 #pragma unroll 8
-    for (uint32_t j = 0; j < kPer; ++j) w.loc += h[b0 + j];
+    for (uint32_t j = 0; j < kPer; ++j) w.loc += h[b0 + ((j + lane) & (kPer - 1u))];
     w.incl = wave_incl_scan(w.loc, lane);
     w.run = w.incl - w.loc;
     return w;
@@ -472,11 +502,12 @@ __device__ __attribute__((always_inline)) inline WaveHist wave_hist(const unsign
 
 // A crossing search's answer, returned by value (out-parameters chosen per path kept these
 // values in scratch memory): found with the bin and the weight before it, or not found with
-// the weight of the whole range searched.
+// the weight of the whole range searched; raw is that weight as the exact fixed-point sum.
 struct Cross {
     int found;
     uint32_t bin;
     double w;
+    unsigned long long raw;
 };
 
 __device__ inline double fx_of(unsigned long long v) { return (double)v / kFx; }
@@ -493,9 +524,13 @@ __device__ __attribute__((always_inline)) inline Cross lane_cross(const unsigned
     const unsigned long long hv = (lane < kPer && bj < limit) ? h[bj] : 0ull;
     const unsigned long long ci = base + wave_incl_scan(hv, lane), ce = ci - hv;
     const unsigned long long at = __ballot(hv != 0ull && fx_of(ce) < target && target <= fx_of(ci));
-    if (at == 0ull) return Cross{0, 0u, fx_of(lane_read(ci, 63))};
+    if (at == 0ull) {
+        const unsigned long long tot = lane_read(ci, 63);
+        return Cross{0, 0u, fx_of(tot), tot};
+    }
     const uint32_t F = (uint32_t)__ffsll((long long)at) - 1u;
-    return Cross{1, L * kPer + F, fx_of(lane_read(ce, (int)F))};
+    const unsigned long long before = lane_read(ce, (int)F);
+    return Cross{1, L * kPer + F, fx_of(before), before};
 }
 
 // Weight-histogram scan from bin 0 up over bins [0, limit) of h (kVBins u64 fixed-point
@@ -510,16 +545,22 @@ __device__ __attribute__((always_inline)) inline Cross wave_cross(const unsigned
     const uint32_t b0 = lane * kPer;
     unsigned long long loc = 0ull;
 #pragma unroll 8
-    for (uint32_t j = 0; j < kPer; ++j) loc += (b0 + j < limit) ? h[b0 + j] : 0ull;
+    for (uint32_t j = 0; j < kPer; ++j) {
+        const uint32_t bj = b0 + ((j + lane) & (kPer - 1u));  // rotated, as in wave_hist
+        loc += (bj < limit) ? h[bj] : 0ull;
+    }
     const unsigned long long incl = wave_incl_scan(loc, lane), run = incl - loc;
     const unsigned long long hit = __ballot(loc != 0ull && fx_of(run) < target && target <= fx_of(incl));
-    if (hit == 0ull) return Cross{0, 0u, fx_of(lane_read(incl, 63))};
+    if (hit == 0ull) {
+        const unsigned long long tot = lane_read(incl, 63);
+        return Cross{0, 0u, fx_of(tot), tot};
+    }
     const uint32_t L = (uint32_t)__ffsll((long long)hit) - 1u;
     const unsigned long long base = lane_read(run, (int)L);
     const Cross r = lane_cross(h, L, base, limit, target);
     if (r.found) return r;
     // unreachable: the sums are monotone and lane L's range holds target
-    return Cross{1, min(L * kPer + kPer - 1u, limit - 1u), fx_of(base)};
+    return Cross{1, min(L * kPer + kPer - 1u, limit - 1u), fx_of(base), base};
 }
 
 // wave_cross over bins [0, limit) of h from its lane sums H (the same answers): lanes whose bins
@@ -537,11 +578,11 @@ __device__ __attribute__((always_inline)) inline Cross wave_cross_pre(const unsi
         const Cross r = lane_cross(h, L, base, limit, target);
         if (r.found) return r;
         // unreachable: the sums are monotone and lane L's range holds target
-        return Cross{1, L * kPer + kPer - 1u, fx_of(base)};
+        return Cross{1, L * kPer + kPer - 1u, fx_of(base), base};
     }
     const unsigned long long base = (Lfull > 0u) ? lane_read(H.incl, (int)Lfull - 1) : 0ull;
     if (Lfull < 64u && Lfull * kPer < limit) return lane_cross(h, Lfull, base, limit, target);
-    return Cross{0, 0u, fx_of(base)};
+    return Cross{0, 0u, fx_of(base), base};
 }
 
 // wave_cross for the whole block: wave 0 scans while the other waves wait at one barrier (a
@@ -578,12 +619,15 @@ struct FvPlan {
     double A;                       // survivor weight (temperature) of the bins above cb
     double target_w, wabove;        // T = 1 nucleus target, and the T = 1 weight above cb
     double total;                   // sum exp(l - m) over the row, from the T = 1 histogram
+    unsigned long long dlo_before;  // temperature weight of the bins above dlo (fixed point)
+    uint32_t dlo_found;             // dlo is the crossing bin of u A (not a clamped fallback)
 };
 
 __device__ inline bool same_weights(const RowCtx& c) { return kLog2e / c.T == kLog2e; }
 
 // Value-bin weight histograms (T = 1 in vm, temperature T in vq) of elements [beg, end).
-__device__ __attribute__((always_inline)) inline void fv_hist(SelShared& s, const RowCtx& c, uint32_t beg, uint32_t end) {
+__device__ __attribute__((always_inline)) inline void fv_hist(SelShared& s, const RowCtx& c, uint32_t beg, uint32_t end,
+                                                              const RowPre* pre = nullptr) {
     const float kq = kLog2e / c.T;
     const bool same = same_weights(c);  // T = 1: one weighting serves nucleus and draw
     for (uint32_t i = threadIdx.x; i < kVBins; i += sel_nt()) { s.vm[i] = 0ull; s.vq[i] = 0ull; }
@@ -594,7 +638,7 @@ __device__ __attribute__((always_inline)) inline void fv_hist(SelShared& s, cons
         const uint32_t b = vbin_d(c, d);
         atomicAdd(&s.vm[b], to_fx(__builtin_amdgcn_exp2f(d * kLog2e)));
         if (!same) atomicAdd(&s.vq[b], to_fx(__builtin_amdgcn_exp2f(d * kq)));
-    });
+    }, pre);
     __syncthreads();
 }
 
@@ -631,12 +675,16 @@ __device__ __attribute__((always_inline)) inline void fv_plan(SelShared& s, cons
         q.wabove = wabove;
         q.u_zero = (u > 0.0f) ? 0u : 1u;
         q.dlo = q.dhi = cb;
+        q.dlo_before = 0ull;
+        q.dlo_found = 0u;
         if (!q.u_zero) {
             const uint32_t lim = (cb < kVBins) ? cb + 1u : kVBins;
             const Cross lo = wave_cross_pre(hq, Hq, lim, (double)u * A);
             const Cross hi = wave_cross_pre(hq, Hq, lim, (double)u * (A + Bq));
             q.dlo = lo.found ? lo.bin : lim - 1u;
             q.dhi = hi.found ? hi.bin : lim - 1u;
+            q.dlo_found = lo.found ? 1u : 0u;
+            q.dlo_before = lo.raw;
         }
         if (threadIdx.x == 0u) *sp = q;
     }
@@ -652,13 +700,14 @@ __device__ inline bool fv_wanted(const RowCtx& c, const FvPlan& P, float v) {
 
 // Appends the elements of [beg, end) in the planned bins to s.cand, counting in s.bu[2]
 // (the count may exceed kCandCap; only the first kCandCap are stored).
-__device__ __attribute__((always_inline)) inline void fv_gather(SelShared& s, const RowCtx& c, const FvPlan& P, uint32_t beg, uint32_t end) {
+__device__ __attribute__((always_inline)) inline void fv_gather(SelShared& s, const RowCtx& c, const FvPlan& P, uint32_t beg, uint32_t end,
+                                                                const RowPre* pre = nullptr) {
     if (threadIdx.x == 0) s.bu[2] = 0u;
     __syncthreads();
     row_pass(c.l + beg, end - beg, [&](float v, uint32_t i) {
         wave_append(&s.bu[2], fv_wanted(c, P, v), ((unsigned long long)(~float_key(v)) << 32) | (beg + i),
                     s.cand, kCandCap);
-    });
+    }, pre);
     __syncthreads();
 }
 
@@ -811,7 +860,19 @@ __device__ __attribute__((always_inline)) inline int fv_finish(SelShared& s, con
     } else {
         uint32_t db;
         double dab;
-        if (!scan_cross(s, hq, cb, r, &db, &dab)) return 0;
+        // The draw's bin lies in [dlo, dhi] unless rounding moved r. When the plan found one bin
+        // there, test r against that bin's exact running sums: the scan over [0, cb) would stop
+        // at the same bin, since every nonempty bin above it ends at or below its start.
+        bool one = false;
+        if (P.dlo == P.dhi && P.dlo_found && P.dlo < cb) {
+            const unsigned long long ce = P.dlo_before, ci = ce + hq[P.dlo];
+            if (hq[P.dlo] != 0ull && fx_of(ce) < r && r <= fx_of(ci)) {
+                db = P.dlo;
+                dab = fx_of(ce);
+                one = true;
+            }
+        }
+        if (!one && !scan_cross(s, hq, cb, r, &db, &dab)) return 0;
         if (db < P.dlo || db > P.dhi) return 0;  // outside the gathered range (rounding)
         if (!fine_cross(s, c, n, db, ~0ull, kq, r - dab, &kt, &bef)) return 0;
     }
@@ -955,13 +1016,16 @@ __global__ __launch_bounds__(kMaxSelThreads) void k_fv_hist(SelectArgs a) {
     const uint32_t k = blockIdx.x, b = blockIdx.y;
     const DevRow row = a.rows[b];
     if (!is_fv_row(row, a.V)) return;
+    uint32_t beg, end;
+    fv_slice(a.V, kFvSlices, k, &beg, &end);
+    const float* lrow = a.logits + (size_t)b * a.V;
+    RowPre pre;
+    row_preload(lrow + beg, end - beg, pre);  // in flight while the row maximum is found
     float m, fmin;
     partial_max_min(s, a.partials + (size_t)b * a.ntile, a.ntile, &m, &fmin);
     if (m == -INFINITY) return;  // degenerate row: k_select reports it
-    const RowCtx c = make_ctx(a.V, a.logits + (size_t)b * a.V, m, fmin, row.temperature, nullptr);
-    uint32_t beg, end;
-    fv_slice(a.V, kFvSlices, k, &beg, &end);
-    fv_hist(s, c, beg, end);
+    const RowCtx c = make_ctx(a.V, lrow, m, fmin, row.temperature, nullptr);
+    fv_hist(s, c, beg, end, &pre);
     // fixed-point bin weights are integers: summing the slices with atomics is exact and
     // order-independent, and k_select reads one 32 KB histogram per row instead of 16
     unsigned long long* acc = a.fv_acc + (size_t)b * 2u * kVBins;
@@ -975,14 +1039,19 @@ __global__ __launch_bounds__(kMaxSelThreads) void k_fv_hist(SelectArgs a) {
 __global__ __launch_bounds__(kMaxSelThreads) void k_fv_gather(SelectArgs a, uint2* __restrict__ scratch) {
     __shared__ SelShared s;
     const uint32_t k = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-    if (!is_fv_row(a.rows[b], a.V)) return;
+    // the row and the hand-over flag in one round trip (the flag of a row that is not a
+    // full-vocabulary row this step may be stale and is not used)
     FvRowState* st = fv_state_of(a, b);
-    if (st->active == 0u) return;
-    const RowCtx c = make_ctx(a.V, a.logits + (size_t)b * a.V, st->m, st->fmin, st->T, scratch + (size_t)b * a.V);
-    const FvPlan P = st->plan;
+    const DevRow row = a.rows[b];
+    const uint32_t active = st->active;
+    if (!is_fv_row(row, a.V) || active == 0u) return;
     uint32_t beg, end;
     fv_slice(a.V, kFvSlices, k, &beg, &end);
-    fv_gather(s, c, P, beg, end);
+    RowPre pre;
+    row_preload(a.logits + (size_t)b * a.V + beg, end - beg, pre);  // in flight while the plan loads
+    const RowCtx c = make_ctx(a.V, a.logits + (size_t)b * a.V, st->m, st->fmin, st->T, scratch + (size_t)b * a.V);
+    const FvPlan P = st->plan;
+    fv_gather(s, c, P, beg, end, &pre);
     const uint32_t nl = s.bu[2];
     __syncthreads();
     if (tid == 0) {
@@ -1005,9 +1074,10 @@ __global__ __launch_bounds__(kMaxSelThreads) void k_fv_gather(SelectArgs a, uint
 __global__ __launch_bounds__(kMaxSelThreads) void k_fv_finish(SelectArgs a, uint2* __restrict__ scratch) {
     __shared__ SelShared s;
     const uint32_t b = blockIdx.x, tid = threadIdx.x;
-    if (!is_fv_row(a.rows[b], a.V)) return;
     FvRowState* st = fv_state_of(a, b);
-    if (st->active == 0u) return;
+    const DevRow row0 = a.rows[b];
+    const uint32_t active = st->active;  // with the row, one round trip (stale unless an fv row)
+    if (!is_fv_row(row0, a.V) || active == 0u) return;
     const RowCtx c = make_ctx(a.V, a.logits + (size_t)b * a.V, st->m, st->fmin, st->T, scratch + (size_t)b * a.V);
     const FvPlan P = st->plan;
     const uint32_t n = st->ncand;
@@ -1046,10 +1116,9 @@ __global__ __launch_bounds__(kMaxSelThreads) void k_fv_finish(SelectArgs a, uint
             rep.r = rr;
             rep.path = 2;
         } else {
-            const DevRow row = a.rows[b];
             RowReport rr = rep;
             uint32_t tk = token;
-            radix_select(s, c, row, st->u, st->want, st->Z, st->arg, &tk, &rr);
+            radix_select(s, c, row0, st->u, st->want, st->Z, st->arg, &tk, &rr);
             rep = rr;
             token = tk;
         }
