@@ -401,7 +401,8 @@ int run_rows(Head& h, HandleBox* bx, const TurboStepInputs* in, const TurboStepO
         throw std::runtime_error("ban_stride must be at least ceil(vocab / 32) words");
 
     tdt::DevRow rows[kMaxBatch];
-    bool all_greedy = true, any_mods = false, any_fv = false, any_short = false;
+    bool all_greedy = true, any_mods = false, any_short = false;
+    tdt::FvList fv;
     for (int b = 0; b < B; ++b) {
         const TurboSamplingRow& r = in->rows[b];
         std::string why;
@@ -412,7 +413,11 @@ int run_rows(Head& h, HandleBox* bx, const TurboStepInputs* in, const TurboStepO
         any_mods = any_mods || mods != 0u;
         all_greedy = all_greedy && r.temperature <= 0.0f;
         rows[b] = make_devrow(h, r, mods);
-        any_fv = any_fv || (rows[b].temperature > 0.0f && rows[b].want >= h.V);
+        if (rows[b].temperature > 0.0f && rows[b].want >= h.V && B <= (int)tdt::kFvMaxBatch) {
+            fv.temp[fv.n] = rows[b].temperature;  // full-vocabulary rows of a small batch
+            fv.row[fv.n] = static_cast<uint8_t>(b);
+            ++fv.n;
+        }
         any_short = any_short || (rows[b].temperature > 0.0f && rows[b].want < h.V);
     }
     uint32_t P = 2;
@@ -496,7 +501,7 @@ int run_rows(Head& h, HandleBox* bx, const TurboStepInputs* in, const TurboStepO
         sa.hist_len = in->history_len;
         sa.hist_overflow = h.overflow_dev;
     }
-    tdt::launch_select(h, B, sa, any_fv, h.stream);
+    tdt::launch_select(h, B, sa, fv, h.stream);
     return 1;
 }
 
@@ -871,7 +876,7 @@ TURBO_DT_API int turbo_lmhead_greedy(void* handle, const void* x, int x_dtype, i
     sa.partials = h.partials;
     sa.rows = h.rows;
     sa.tokens = tokens;
-    tdt::launch_select(h, batch, sa, false, h.stream);
+    tdt::launch_select(h, batch, sa, tdt::FvList{}, h.stream);
     return 1;
     API_CATCH(0)
 }

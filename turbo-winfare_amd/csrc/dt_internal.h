@@ -266,8 +266,16 @@ constexpr uint32_t kFvCandCap = 8192;
 constexpr size_t kFvStateBytes = 128;
 // TurboRowReport.status bit: the row's history was full, so its token was not appended.
 constexpr uint32_t kStatusHistoryFull = 1u;
-// any_fv: some row takes the full-vocabulary value path (sampled, shortlist lifted).
-void launch_select(const Head& h, int batch, const SelectArgs& a, bool any_fv, hipStream_t st);
+// The rows that take the full-vocabulary value path (sampled, shortlist lifted), with their
+// temperatures, in ascending row order. Batches up to kFvMaxBatch rows split these rows' passes
+// over several workgroups, which take their row from this list in the kernel arguments.
+struct FvList {
+    uint32_t n = 0;
+    float temp[kFvMaxBatch];
+    uint8_t row[kFvMaxBatch];
+};
+static_assert(kFvMaxBatch <= 256, "row indices of the list are bytes");
+void launch_select(const Head& h, int batch, const SelectArgs& a, const FvList& fv, hipStream_t st);
 
 // misc.hip
 void launch_softcap(float* z, size_t n, float cap, hipStream_t st);

@@ -502,12 +502,11 @@ __device__ __attribute__((always_inline)) inline WaveHist wave_hist(const unsign
 
 // A crossing search's answer, returned by value (out-parameters chosen per path kept these
 // values in scratch memory): found with the bin and the weight before it, or not found with
-// the weight of the whole range searched; raw is that weight as the exact fixed-point sum.
+// the weight of the whole range searched.
 struct Cross {
     int found;
     uint32_t bin;
     double w;
-    unsigned long long raw;
 };
 
 __device__ inline double fx_of(unsigned long long v) { return (double)v / kFx; }
@@ -524,13 +523,9 @@ __device__ __attribute__((always_inline)) inline Cross lane_cross(const unsigned
     const unsigned long long hv = (lane < kPer && bj < limit) ? h[bj] : 0ull;
     const unsigned long long ci = base + wave_incl_scan(hv, lane), ce = ci - hv;
     const unsigned long long at = __ballot(hv != 0ull && fx_of(ce) < target && target <= fx_of(ci));
-    if (at == 0ull) {
-        const unsigned long long tot = lane_read(ci, 63);
-        return Cross{0, 0u, fx_of(tot), tot};
-    }
+    if (at == 0ull) return Cross{0, 0u, fx_of(lane_read(ci, 63))};
     const uint32_t F = (uint32_t)__ffsll((long long)at) - 1u;
-    const unsigned long long before = lane_read(ce, (int)F);
-    return Cross{1, L * kPer + F, fx_of(before), before};
+    return Cross{1, L * kPer + F, fx_of(lane_read(ce, (int)F))};
 }
 
 // Weight-histogram scan from bin 0 up over bins [0, limit) of h (kVBins u64 fixed-point
@@ -551,16 +546,13 @@ __device__ __attribute__((always_inline)) inline Cross wave_cross(const unsigned
     }
     const unsigned long long incl = wave_incl_scan(loc, lane), run = incl - loc;
     const unsigned long long hit = __ballot(loc != 0ull && fx_of(run) < target && target <= fx_of(incl));
-    if (hit == 0ull) {
-        const unsigned long long tot = lane_read(incl, 63);
-        return Cross{0, 0u, fx_of(tot), tot};
-    }
+    if (hit == 0ull) return Cross{0, 0u, fx_of(lane_read(incl, 63))};
     const uint32_t L = (uint32_t)__ffsll((long long)hit) - 1u;
     const unsigned long long base = lane_read(run, (int)L);
     const Cross r = lane_cross(h, L, base, limit, target);
     if (r.found) return r;
     // unreachable: the sums are monotone and lane L's range holds target
-    return Cross{1, min(L * kPer + kPer - 1u, limit - 1u), fx_of(base), base};
+    return Cross{1, min(L * kPer + kPer - 1u, limit - 1u), fx_of(base)};
 }
 
 // wave_cross over bins [0, limit) of h from its lane sums H (the same answers): lanes whose bins
@@ -578,11 +570,11 @@ __device__ __attribute__((always_inline)) inline Cross wave_cross_pre(const unsi
         const Cross r = lane_cross(h, L, base, limit, target);
         if (r.found) return r;
         // unreachable: the sums are monotone and lane L's range holds target
-        return Cross{1, L * kPer + kPer - 1u, fx_of(base), base};
+        return Cross{1, L * kPer + kPer - 1u, fx_of(base)};
     }
     const unsigned long long base = (Lfull > 0u) ? lane_read(H.incl, (int)Lfull - 1) : 0ull;
     if (Lfull < 64u && Lfull * kPer < limit) return lane_cross(h, Lfull, base, limit, target);
-    return Cross{0, 0u, fx_of(base), base};
+    return Cross{0, 0u, fx_of(base)};
 }
 
 // wave_cross for the whole block: wave 0 scans while the other waves wait at one barrier (a
@@ -684,7 +676,12 @@ __device__ __attribute__((always_inline)) inline void fv_plan(SelShared& s, cons
             q.dlo = lo.found ? lo.bin : lim - 1u;
             q.dhi = hi.found ? hi.bin : lim - 1u;
             q.dlo_found = lo.found ? 1u : 0u;
-            q.dlo_before = lo.raw;
+            // exact fixed-point weight of the bins above dlo: the lane sums before its lane, then
+            // that lane's bins up to dlo
+            constexpr uint32_t kPer = kVBins / 64u;
+            const uint32_t lane = threadIdx.x & 63u, L = q.dlo / kPer, r = q.dlo % kPer;
+            const unsigned long long part = (lane < r) ? hq[L * kPer + lane] : 0ull;
+            q.dlo_before = lane_read(Hq.run, (int)L) + lane_read(wave_incl_scan(part, lane), 63);
         }
         if (threadIdx.x == 0u) *sp = q;
     }
@@ -1011,11 +1008,11 @@ __device__ inline FvRowState* fv_state_of(const SelectArgs& a, uint32_t b) {
 }
 
 // Slice histograms of the full-vocabulary rows: workgroup (k, b) bins slice k of row b.
-__global__ __launch_bounds__(kMaxSelThreads) void k_fv_hist(SelectArgs a) {
+__global__ __launch_bounds__(kMaxSelThreads) void k_fv_hist(SelectArgs a, FvList fv) {
     __shared__ SelShared s;
-    const uint32_t k = blockIdx.x, b = blockIdx.y;
-    const DevRow row = a.rows[b];
-    if (!is_fv_row(row, a.V)) return;
+    // the row and its temperature come with the launch: the first loads are the row's own
+    const uint32_t k = blockIdx.x, b = fv.row[blockIdx.y];
+    const float T = fv.temp[blockIdx.y];
     uint32_t beg, end;
     fv_slice(a.V, kFvSlices, k, &beg, &end);
     const float* lrow = a.logits + (size_t)b * a.V;
@@ -1024,7 +1021,7 @@ __global__ __launch_bounds__(kMaxSelThreads) void k_fv_hist(SelectArgs a) {
     float m, fmin;
     partial_max_min(s, a.partials + (size_t)b * a.ntile, a.ntile, &m, &fmin);
     if (m == -INFINITY) return;  // degenerate row: k_select reports it
-    const RowCtx c = make_ctx(a.V, lrow, m, fmin, row.temperature, nullptr);
+    const RowCtx c = make_ctx(a.V, lrow, m, fmin, T, nullptr);
     fv_hist(s, c, beg, end, &pre);
     // fixed-point bin weights are integers: summing the slices with atomics is exact and
     // order-independent, and k_select reads one 32 KB histogram per row instead of 16
@@ -1036,21 +1033,20 @@ __global__ __launch_bounds__(kMaxSelThreads) void k_fv_hist(SelectArgs a) {
 }
 
 // Gather of the planned bins, slice k of row b, into the row's global candidate list.
-__global__ __launch_bounds__(kMaxSelThreads) void k_fv_gather(SelectArgs a, uint2* __restrict__ scratch) {
+__global__ __launch_bounds__(kMaxSelThreads) void k_fv_gather(SelectArgs a, FvList fv, uint2* __restrict__ scratch) {
     __shared__ SelShared s;
-    const uint32_t k = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-    // the row and the hand-over flag in one round trip (the flag of a row that is not a
-    // full-vocabulary row this step may be stale and is not used)
-    FvRowState* st = fv_state_of(a, b);
-    const DevRow row = a.rows[b];
-    const uint32_t active = st->active;
-    if (!is_fv_row(row, a.V) || active == 0u) return;
+    const uint32_t k = blockIdx.x, b = fv.row[blockIdx.y], tid = threadIdx.x;
     uint32_t beg, end;
     fv_slice(a.V, kFvSlices, k, &beg, &end);
     RowPre pre;
-    row_preload(a.logits + (size_t)b * a.V + beg, end - beg, pre);  // in flight while the plan loads
-    const RowCtx c = make_ctx(a.V, a.logits + (size_t)b * a.V, st->m, st->fmin, st->T, scratch + (size_t)b * a.V);
+    row_preload(a.logits + (size_t)b * a.V + beg, end - beg, pre);
+    // the plan in the same round trip as the slice's first loads (read before the branch)
+    FvRowState* st = fv_state_of(a, b);
+    const uint32_t active = st->active;
     const FvPlan P = st->plan;
+    const float m = st->m, fmin = st->fmin, T = st->T;
+    if (active == 0u) return;  // k_select finished the row
+    const RowCtx c = make_ctx(a.V, a.logits + (size_t)b * a.V, m, fmin, T, scratch + (size_t)b * a.V);
     fv_gather(s, c, P, beg, end, &pre);
     const uint32_t nl = s.bu[2];
     __syncthreads();
@@ -1071,34 +1067,46 @@ __global__ __launch_bounds__(kMaxSelThreads) void k_fv_gather(SelectArgs a, uint
 
 // Sort of the gathered candidates and the draw, one workgroup per deferred row (the kernel
 // boundary orders it after every slice's stores).
-__global__ __launch_bounds__(kMaxSelThreads) void k_fv_finish(SelectArgs a, uint2* __restrict__ scratch) {
+__global__ __launch_bounds__(kMaxSelThreads) void k_fv_finish(SelectArgs a, FvList fv, uint2* __restrict__ scratch) {
+    constexpr uint32_t kCandPer = kCandCap / kMaxSelThreads, kHistPer = 2u * kVBins / kMaxSelThreads;
+    static_assert(kCandCap % kMaxSelThreads == 0u && kVBins % kMaxSelThreads == 0u,
+                  "the finish loads whole rounds of candidates and bins");
     __shared__ SelShared s;
-    const uint32_t b = blockIdx.x, tid = threadIdx.x;
-    FvRowState* st = fv_state_of(a, b);
-    const DevRow row0 = a.rows[b];
-    const uint32_t active = st->active;  // with the row, one round trip (stale unless an fv row)
-    if (!is_fv_row(row0, a.V) || active == 0u) return;
-    const RowCtx c = make_ctx(a.V, a.logits + (size_t)b * a.V, st->m, st->fmin, st->T, scratch + (size_t)b * a.V);
-    const FvPlan P = st->plan;
-    const uint32_t n = st->ncand;
+    const uint32_t b = fv.row[blockIdx.x], tid = threadIdx.x;
+    // Everything the finish reads, in one round trip: the row's state, its merged histograms and
+    // every candidate slot (slots past the gathered count hold an earlier step's and are dropped).
+    const FvRowState sv = *fv_state_of(a, b);
+    const unsigned long long* cg = a.fv_cand + (size_t)b * kCandCap;
+    const unsigned long long* mg = a.fv_merged + (size_t)b * 2u * kVBins;
+    unsigned long long cv[kCandPer], hv[kHistPer];
+#pragma unroll
+    for (uint32_t j = 0; j < kCandPer; ++j) cv[j] = cg[tid + j * kMaxSelThreads];
+#pragma unroll
+    for (uint32_t j = 0; j < kHistPer; ++j) hv[j] = mg[tid + j * kMaxSelThreads];
+    if (sv.active == 0u) return;  // k_select finished the row
+    const RowCtx c = make_ctx(a.V, a.logits + (size_t)b * a.V, sv.m, sv.fmin, sv.T, scratch + (size_t)b * a.V);
+    const uint32_t n = sv.ncand;
     RowReport rep = {};
-    rep.max_logit = st->m;
-    rep.u = st->u;
-    rep.shortlist = st->want;
-    rep.total = st->Z;
-    uint32_t token = st->arg;
+    rep.max_logit = sv.m;
+    rep.u = sv.u;
+    rep.shortlist = sv.want;
+    rep.total = sv.Z;
+    uint32_t token = sv.arg;
     int ok = 0;
-    if (st->overflow == 0u && n > 0u && n <= kCandCap) {
-        for (uint32_t i = tid; i < n; i += sel_nt()) s.cand[i] = a.fv_cand[(size_t)b * kCandCap + i];
-        const unsigned long long* mg = a.fv_merged + (size_t)b * 2u * kVBins;
-        for (uint32_t i = tid; i < kVBins; i += sel_nt()) {
-            s.vm[i] = mg[i];
-            s.vq[i] = mg[kVBins + i];
+    if (sv.overflow == 0u && n > 0u && n <= kCandCap) {
+#pragma unroll
+        for (uint32_t j = 0; j < kCandPer; ++j)
+            if (tid + j * kMaxSelThreads < n) s.cand[tid + j * kMaxSelThreads] = cv[j];
+#pragma unroll
+        for (uint32_t j = 0; j < kHistPer; ++j) {
+            const uint32_t i = tid + j * kMaxSelThreads;
+            if (i < kVBins) s.vm[i] = hv[j];
+            else s.vq[i - kVBins] = hv[j];
         }
         __syncthreads();
         double dn = 0.0, rr = 0.0;
         uint32_t tk = 0;
-        ok = fv_finish(s, c, P, n, st->u, &tk, &dn, &rr);
+        ok = fv_finish(s, c, sv.plan, n, sv.u, &tk, &dn, &rr);
         if (ok) {
             token = tk;
             rep.denom = dn;
@@ -1110,15 +1118,16 @@ __global__ __launch_bounds__(kMaxSelThreads) void k_fv_finish(SelectArgs a, uint
         // too many candidates, or rounding outside the gathered bins: the one-workgroup paths
         double dn = 0.0, rr = 0.0, zt = 0.0;
         uint32_t tk = 0;
-        if (full_vocab_value_path(s, c, st->top_p, st->u, st->arg, &tk, &dn, &rr, &zt)) {
+        if (full_vocab_value_path(s, c, sv.top_p, sv.u, sv.arg, &tk, &dn, &rr, &zt)) {
             token = tk;
             rep.denom = dn;
             rep.r = rr;
             rep.path = 2;
         } else {
+            const DevRow row = a.rows[b];
             RowReport rr = rep;
             uint32_t tk = token;
-            radix_select(s, c, row0, st->u, st->want, st->Z, st->arg, &tk, &rr);
+            radix_select(s, c, row, sv.u, sv.want, sv.Z, sv.arg, &tk, &rr);
             rep = rr;
             token = tk;
         }
@@ -1607,24 +1616,25 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
     if (!deferred) write_row(a, b, token, rep, hlen);
 }
 
-void launch_select(const Head& h, int batch, const SelectArgs& args, bool any_fv, hipStream_t st) {
+void launch_select(const Head& h, int batch, const SelectArgs& args, const FvList& fv, hipStream_t st) {
     SelectArgs a = args;
-    const bool multi = any_fv && (uint32_t)batch <= kFvMaxBatch && h.fv_acc;
+    if (fv.n > kFvMaxBatch || fv.n > (uint32_t)batch) throw std::runtime_error("full-vocabulary row list too long");
+    const bool multi = fv.n > 0u && (uint32_t)batch <= kFvMaxBatch && h.fv_acc;
     a.fv_acc = multi ? h.fv_acc : nullptr;
     a.fv_merged = h.fv_merged;
     a.fv_cand = h.fv_cand;
     a.fv_state = h.fv_state;
     uint2* scratch = reinterpret_cast<uint2*>(h.list_scratch);
     if (multi) {
-        hipLaunchKernelGGL(k_fv_hist, dim3(kFvSlices, (unsigned)batch), dim3(kMaxSelThreads), 0, st, a);
+        hipLaunchKernelGGL(k_fv_hist, dim3(kFvSlices, fv.n), dim3(kMaxSelThreads), 0, st, a, fv);
         check_hip(hipGetLastError(), "select (slice histograms)");
     }
     hipLaunchKernelGGL(k_select<kMaxSelThreads>, dim3((unsigned)batch), dim3(kMaxSelThreads), 0, st, a, scratch);
     check_hip(hipGetLastError(), "select");
     if (multi) {
-        hipLaunchKernelGGL(k_fv_gather, dim3(kFvSlices, (unsigned)batch), dim3(kMaxSelThreads), 0, st, a, scratch);
+        hipLaunchKernelGGL(k_fv_gather, dim3(kFvSlices, fv.n), dim3(kMaxSelThreads), 0, st, a, fv, scratch);
         check_hip(hipGetLastError(), "select (slice gather)");
-        hipLaunchKernelGGL(k_fv_finish, dim3((unsigned)batch), dim3(kMaxSelThreads), 0, st, a, scratch);
+        hipLaunchKernelGGL(k_fv_finish, dim3(fv.n), dim3(kMaxSelThreads), 0, st, a, fv, scratch);
         check_hip(hipGetLastError(), "select (finish)");
     }
 }
