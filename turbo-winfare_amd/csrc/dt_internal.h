@@ -258,9 +258,14 @@ struct SelectArgs {
     unsigned long long* fv_cand;    // [B][kFvCandCap] gathered candidates
     void* fv_state;                 // [B] x kFvStateBytes per-row plan and counters
 };
-// Small batches split each full-vocabulary row's two passes over kFvSlices workgroups.
+// Small batches split each full-vocabulary row's two passes over several workgroups (slices):
+// about kFvSliceBudget workgroups in all, from kFvMinSlices to kFvMaxSlices per row. More
+// slices shorten each workgroup's pass, but every slice adds its histogram into the row's sums
+// with global atomics, which contend once thousands of workgroups do it.
 constexpr uint32_t kFvMaxBatch = 64;
-constexpr uint32_t kFvSlices = 16;
+constexpr uint32_t kFvSliceBudget = 256;
+constexpr uint32_t kFvMinSlices = 4;
+constexpr uint32_t kFvMaxSlices = 32;
 constexpr uint32_t kFvBins = 2048;
 constexpr uint32_t kFvCandCap = 8192;
 constexpr size_t kFvStateBytes = 128;

@@ -32,6 +32,7 @@
 // row maximum are <= 1): integer LDS atomics run an order of magnitude faster than float ones
 // on gfx950. Truncation changes a row total by at most V * 2^-40 relative. Scans of those
 // histograms add exact integer sums.
+#include <algorithm>
 #include <stdexcept>
 
 #include "dt_internal.h"
@@ -1014,7 +1015,7 @@ __global__ __launch_bounds__(kMaxSelThreads) void k_fv_hist(SelectArgs a, FvList
     const uint32_t k = blockIdx.x, b = fv.row[blockIdx.y];
     const float T = fv.temp[blockIdx.y];
     uint32_t beg, end;
-    fv_slice(a.V, kFvSlices, k, &beg, &end);
+    fv_slice(a.V, gridDim.x, k, &beg, &end);  // the grid's x extent is the slice count
     const float* lrow = a.logits + (size_t)b * a.V;
     RowPre pre;
     row_preload(lrow + beg, end - beg, pre);  // in flight while the row maximum is found
@@ -1037,7 +1038,7 @@ __global__ __launch_bounds__(kMaxSelThreads) void k_fv_gather(SelectArgs a, FvLi
     __shared__ SelShared s;
     const uint32_t k = blockIdx.x, b = fv.row[blockIdx.y], tid = threadIdx.x;
     uint32_t beg, end;
-    fv_slice(a.V, kFvSlices, k, &beg, &end);
+    fv_slice(a.V, gridDim.x, k, &beg, &end);
     RowPre pre;
     row_preload(a.logits + (size_t)b * a.V + beg, end - beg, pre);
     // the plan in the same round trip as the slice's first loads (read before the branch)
@@ -1620,19 +1621,20 @@ void launch_select(const Head& h, int batch, const SelectArgs& args, const FvLis
     SelectArgs a = args;
     if (fv.n > kFvMaxBatch || fv.n > (uint32_t)batch) throw std::runtime_error("full-vocabulary row list too long");
     const bool multi = fv.n > 0u && (uint32_t)batch <= kFvMaxBatch && h.fv_acc;
+    const uint32_t slices = multi ? std::min(kFvMaxSlices, std::max(kFvMinSlices, kFvSliceBudget / fv.n)) : 0u;
     a.fv_acc = multi ? h.fv_acc : nullptr;
     a.fv_merged = h.fv_merged;
     a.fv_cand = h.fv_cand;
     a.fv_state = h.fv_state;
     uint2* scratch = reinterpret_cast<uint2*>(h.list_scratch);
     if (multi) {
-        hipLaunchKernelGGL(k_fv_hist, dim3(kFvSlices, fv.n), dim3(kMaxSelThreads), 0, st, a, fv);
+        hipLaunchKernelGGL(k_fv_hist, dim3(slices, fv.n), dim3(kMaxSelThreads), 0, st, a, fv);
         check_hip(hipGetLastError(), "select (slice histograms)");
     }
     hipLaunchKernelGGL(k_select<kMaxSelThreads>, dim3((unsigned)batch), dim3(kMaxSelThreads), 0, st, a, scratch);
     check_hip(hipGetLastError(), "select");
     if (multi) {
-        hipLaunchKernelGGL(k_fv_gather, dim3(kFvSlices, fv.n), dim3(kMaxSelThreads), 0, st, a, fv, scratch);
+        hipLaunchKernelGGL(k_fv_gather, dim3(slices, fv.n), dim3(kMaxSelThreads), 0, st, a, fv, scratch);
         check_hip(hipGetLastError(), "select (slice gather)");
         hipLaunchKernelGGL(k_fv_finish, dim3(fv.n), dim3(kMaxSelThreads), 0, st, a, fv, scratch);
         check_hip(hipGetLastError(), "select (finish)");
