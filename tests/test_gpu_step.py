@@ -628,7 +628,7 @@ def test_sampler_vocabulary_past_register_tiles(kind):
 
 
 def test_full_vocab_one_workgroup_path(head):
-    """Batches above 64 rows take the one-workgroup full-vocabulary path (histogram pass, plan,
+    """Steps with more than 64 full-vocabulary rows take the one-workgroup path (histogram pass, plan,
     gather pass, finish in one workgroup per row) instead of the multi-workgroup one. Half the
     rows hold a first eighth far below the rest (below the value bins' range, so in the last
     bin). Every row gives the oracle sampler's token."""
@@ -644,6 +644,36 @@ def test_full_vocab_one_workgroup_path(head):
     check_sampler_on_gpu_logits(rows, toks, base, [T.row_uniform(r) for r in rows])
     paths = rep.view(np.uint32)[:, 5]
     assert np.all(paths == 2), paths
+
+
+def test_few_full_vocab_rows_in_a_large_batch(head):
+    """A batch above 64 rows with only a few full-vocabulary rows (here 100 rows, of which rows 3,
+    50 and 99 sample the whole vocabulary and row 64 is degenerate): those rows still take the
+    multi-workgroup path, whose per-row buffers cover every row of the largest batch. The other
+    rows are greedy and shortlist rows. Every row gives the oracle sampler's token."""
+    h, _ = head
+    Bn = 100
+    base = (synth.normal(9, 84, Bn * V).reshape(Bn, V) * 3).astype(np.float32)
+    fv_rows = {3: (1.0, 0.9), 50: (0.8, 0.95), 64: (1.0, 0.9), 99: (1.2, 0.7)}
+    base[64] = -np.inf
+    rows = []
+    for b in range(Bn):
+        if b in fv_rows:
+            t, p = fv_rows[b]
+            rows.append(T.row_default(temperature=t, top_p=p, top_k=0, seed=700 + b, counter=4,
+                                      flags=T.TURBO_ROW_FULL_VOCAB))
+        elif b % 5 == 0:
+            rows.append(T.row_default())
+        else:
+            rows.append(T.row_default(temperature=0.9, top_p=0.9, top_k=[10, 40, 64, 200][b % 4], seed=700 + b,
+                                      counter=4))
+    toks, after, rep = sample_given(h, base, rows)
+    assert np.array_equal(after[np.arange(Bn) != 64], base[np.arange(Bn) != 64])
+    assert int(toks[64]) == 0xFFFFFFFF
+    live = [b for b in range(Bn) if b != 64]
+    check_sampler_on_gpu_logits([rows[b] for b in live], toks[live], base[live], [T.row_uniform(rows[b]) for b in live])
+    paths = rep.view(np.uint32)[:, 5]
+    assert all(paths[b] == 2 for b in (3, 50, 99)) and paths[64] == 3, paths
 
 
 def test_full_history_reports_and_fails_the_next_sync(head):

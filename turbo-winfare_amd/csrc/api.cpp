@@ -403,6 +403,7 @@ int run_rows(Head& h, HandleBox* bx, const TurboStepInputs* in, const TurboStepO
     tdt::DevRow rows[kMaxBatch];
     bool all_greedy = true, any_mods = false, any_short = false;
     tdt::FvList fv;
+    uint32_t n_fv = 0;
     for (int b = 0; b < B; ++b) {
         const TurboSamplingRow& r = in->rows[b];
         std::string why;
@@ -413,13 +414,16 @@ int run_rows(Head& h, HandleBox* bx, const TurboStepInputs* in, const TurboStepO
         any_mods = any_mods || mods != 0u;
         all_greedy = all_greedy && r.temperature <= 0.0f;
         rows[b] = make_devrow(h, r, mods);
-        if (rows[b].temperature > 0.0f && rows[b].want >= h.V && B <= (int)tdt::kFvMaxBatch) {
-            fv.temp[fv.n] = rows[b].temperature;  // full-vocabulary rows of a small batch
-            fv.row[fv.n] = static_cast<uint8_t>(b);
-            ++fv.n;
+        if (rows[b].temperature > 0.0f && rows[b].want >= h.V) {  // full-vocabulary rows
+            if (n_fv < tdt::kFvMaxRows) {
+                fv.temp[n_fv] = rows[b].temperature;
+                fv.row[n_fv] = static_cast<uint8_t>(b);
+            }
+            ++n_fv;
         }
         any_short = any_short || (rows[b].temperature > 0.0f && rows[b].want < h.V);
     }
+    fv.n = (n_fv <= tdt::kFvMaxRows) ? n_fv : 0u;  // many such rows: one workgroup per row
     uint32_t P = 2;
     if (has_bias) P = tdt::modtable_sort_size(h, in->bias_stride);
     float* logits = given_logits ? given_logits : (out->logits ? out->logits : (all_greedy ? nullptr : h.logits));
@@ -677,14 +681,12 @@ TURBO_DT_API void* turbo_lmhead_create(const TurboLMHeadDesc* d) {
         check_hip(hipMemsetAsync(h.hcount, 0, MB * h.V * sizeof(uint32_t), cs.s), "clear history counts");
         check_hip(hipMemsetAsync(h.hbits, 0, MB * h.hbw * sizeof(uint32_t), cs.s), "clear history bitmap");
         h.list_scratch = dalloc<uint2>(MB * h.V, "alloc list scratch");
-        h.fv_acc = dalloc<unsigned long long>((size_t)tdt::kFvMaxBatch * 2u * tdt::kFvBins,
-                                              "alloc select slice-histogram sums");
-        check_hip(hipMemsetAsync(h.fv_acc, 0, (size_t)tdt::kFvMaxBatch * 2u * tdt::kFvBins * 8u, cs.s),
-                  "clear select slice-histogram sums");
-        h.fv_merged = dalloc<unsigned long long>((size_t)tdt::kFvMaxBatch * 2u * tdt::kFvBins, "alloc select histograms");
-        h.fv_cand = dalloc<unsigned long long>((size_t)tdt::kFvMaxBatch * tdt::kFvCandCap, "alloc select candidates");
-        h.fv_state = dalloc<unsigned char>((size_t)tdt::kFvMaxBatch * tdt::kFvStateBytes, "alloc select state");
-        check_hip(hipMemsetAsync(h.fv_state, 0, (size_t)tdt::kFvMaxBatch * tdt::kFvStateBytes, cs.s),
+        h.fv_acc = dalloc<unsigned long long>(MB * 2u * tdt::kFvBins, "alloc select slice-histogram sums");
+        check_hip(hipMemsetAsync(h.fv_acc, 0, MB * 2u * tdt::kFvBins * 8u, cs.s), "clear select slice-histogram sums");
+        h.fv_merged = dalloc<unsigned long long>(MB * 2u * tdt::kFvBins, "alloc select histograms");
+        h.fv_cand = dalloc<unsigned long long>(MB * tdt::kFvCandCap, "alloc select candidates");
+        h.fv_state = dalloc<unsigned char>(MB * tdt::kFvStateBytes, "alloc select state");
+        check_hip(hipMemsetAsync(h.fv_state, 0, MB * tdt::kFvStateBytes, cs.s),
                   "clear select state");
         check_hip(hipHostMalloc(reinterpret_cast<void**>(&h.ring_host),
                                 sizeof(tdt::DevRow) * MB * Head::kRing,

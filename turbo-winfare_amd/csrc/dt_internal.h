@@ -65,10 +65,10 @@ struct Head {
     uint32_t* mod_count = nullptr;     // [max_batch]
     uint32_t* block_start = nullptr;   // [max_batch][ntile + 1]
     void* list_scratch = nullptr;      // [max_batch][V] uint2 compaction lists (select)
-    unsigned long long* fv_acc = nullptr;     // [kFvMaxBatch][2][kFvBins], zero between steps
-    unsigned long long* fv_merged = nullptr;  // [kFvMaxBatch][2][kFvBins]
-    unsigned long long* fv_cand = nullptr;    // [kFvMaxBatch][kFvCandCap]
-    void* fv_state = nullptr;                 // [kFvMaxBatch] x kFvStateBytes
+    unsigned long long* fv_acc = nullptr;     // [max_batch][2][kFvBins], zero between steps
+    unsigned long long* fv_merged = nullptr;  // [max_batch][2][kFvBins]
+    unsigned long long* fv_cand = nullptr;    // [max_batch][kFvCandCap]
+    void* fv_state = nullptr;                 // [max_batch] x kFvStateBytes
 
     // Host staging ring for DevRow uploads (pinned).
     // Rows of batches above kInlineRows are staged in a ring of pinned slots, reused group by
@@ -258,11 +258,12 @@ struct SelectArgs {
     unsigned long long* fv_cand;    // [B][kFvCandCap] gathered candidates
     void* fv_state;                 // [B] x kFvStateBytes per-row plan and counters
 };
-// Small batches split each full-vocabulary row's two passes over several workgroups (slices):
-// about kFvSliceBudget workgroups in all, from kFvMinSlices to kFvMaxSlices per row. More
-// slices shorten each workgroup's pass, but every slice adds its histogram into the row's sums
-// with global atomics, which contend once thousands of workgroups do it.
-constexpr uint32_t kFvMaxBatch = 64;
+// Steps with at most kFvMaxRows full-vocabulary rows split each such row's two passes over
+// several workgroups (slices): about kFvSliceBudget workgroups in all, from kFvMinSlices to
+// kFvMaxSlices per row. More slices shorten each workgroup's pass, but every slice adds its
+// histogram into the row's sums with global atomics, which contend once thousands of workgroups
+// do it. More such rows than kFvMaxRows take one workgroup per row.
+constexpr uint32_t kFvMaxRows = 64;
 constexpr uint32_t kFvSliceBudget = 256;
 constexpr uint32_t kFvMinSlices = 4;
 constexpr uint32_t kFvMaxSlices = 32;
@@ -272,14 +273,13 @@ constexpr size_t kFvStateBytes = 128;
 // TurboRowReport.status bit: the row's history was full, so its token was not appended.
 constexpr uint32_t kStatusHistoryFull = 1u;
 // The rows that take the full-vocabulary value path (sampled, shortlist lifted), with their
-// temperatures, in ascending row order. Batches up to kFvMaxBatch rows split these rows' passes
-// over several workgroups, which take their row from this list in the kernel arguments.
+// temperatures, in ascending row order, when there are at most kFvMaxRows of them (else n = 0).
+// The multi-workgroup kernels take their row from this list in the kernel arguments.
 struct FvList {
     uint32_t n = 0;
-    float temp[kFvMaxBatch];
-    uint8_t row[kFvMaxBatch];
+    float temp[kFvMaxRows];
+    uint8_t row[kFvMaxRows];  // row indices below 256, the largest batch
 };
-static_assert(kFvMaxBatch <= 256, "row indices of the list are bytes");
 void launch_select(const Head& h, int batch, const SelectArgs& a, const FvList& fv, hipStream_t st);
 
 // misc.hip

@@ -29,7 +29,7 @@ constexpr uint32_t kNaBatch = TURBO_NOALLOC_MAX_BATCH;
 constexpr uint32_t kNaVocab = TURBO_NOALLOC_MAX_VOCAB;
 constexpr uint32_t kNaTiles = kNaVocab / kTileRows;
 constexpr uint32_t kNaWords = kNaVocab / 32;
-static_assert(kNaVocab % kTileRows == 0 && kNaBatch <= (uint32_t)kInlineRows && kNaBatch <= kFvMaxBatch,
+static_assert(kNaVocab % kTileRows == 0 && kNaBatch <= (uint32_t)kInlineRows && kNaBatch <= kFvMaxRows,
               "rows ride in the kernel arguments; the full-vocabulary state covers every row");
 
 constexpr size_t align256(size_t n) { return (n + 255u) & ~size_t(255); }

@@ -22,8 +22,8 @@
 //             [lo, max] (bin order is rank order); one wave plans the nucleus bin and the bins
 //             the draw can land in (bounded before the cut is known), whose elements a second
 //             pass gathers. The crossings inside a bin are narrowed by 2048 sub-bins and resolved
-//             exactly over a sorted sub-bin. Batches up to 64 rows split each such row's passes
-//             over 16 workgroups (k_fv_hist, k_fv_gather, k_fv_finish).
+//             exactly over a sorted sub-bin. Steps with at most 64 such rows split each one's
+//             passes over 4 - 32 workgroups (k_fv_hist, k_fv_gather, k_fv_finish).
 //  fallback   shortlist overflow or a bin too large to gather (massive ties): weighted radix
 //             select over the order-preserving keys, with ties among equal keys (equal
 //             weights) resolved by count and a radix select over ids.
@@ -1619,8 +1619,9 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
 
 void launch_select(const Head& h, int batch, const SelectArgs& args, const FvList& fv, hipStream_t st) {
     SelectArgs a = args;
-    if (fv.n > kFvMaxBatch || fv.n > (uint32_t)batch) throw std::runtime_error("full-vocabulary row list too long");
-    const bool multi = fv.n > 0u && (uint32_t)batch <= kFvMaxBatch && h.fv_acc;
+    if (fv.n > kFvMaxRows || fv.n > (uint32_t)batch || (fv.n && batch > 256))
+        throw std::runtime_error("full-vocabulary row list too long");
+    const bool multi = fv.n > 0u && h.fv_acc;
     const uint32_t slices = multi ? std::min(kFvMaxSlices, std::max(kFvMinSlices, kFvSliceBudget / fv.n)) : 0u;
     a.fv_acc = multi ? h.fv_acc : nullptr;
     a.fv_merged = h.fv_merged;
