@@ -1503,36 +1503,80 @@ __global__ __launch_bounds__(NT) void k_select(SelectArgs a, uint2* __restrict__
                         denom = s.bd[1];
                         r = s.bd[2];
                     } else {
-                        float li = -INFINITY;
-                        uint32_t idi = 0;
-                        double pv = 0.0, qv = 0.0;
+                        // 64 < W <= kMaxTopK: the threads below W compute their entries' two
+                        // exponentials side by side, then wave 0 scans them four to a lane
+                        // (consecutive entries, so each lane's running sums plus a wave scan of
+                        // the lane totals are the running sums in rank order) and picks the cut
+                        // and the draw as above: two barriers instead of the block scans' eight
+                        constexpr uint32_t kPer = kMaxTopK / 64u;
+                        static_assert(2u * kMaxTopK * sizeof(double) <= sizeof(s.vm), "entries fit the bins");
+                        double* pd = reinterpret_cast<double*>(s.vm);  // the window counts are spent
+                        double* qd = pd + kMaxTopK;
                         if (tid < W) {
                             const unsigned long long cv = s.cand[tid];
-                            li = key_float(~(uint32_t)(cv >> 32));
-                            idi = (uint32_t)cv;
-                            const double dl = (double)li - (double)m;
-                            pv = exp(dl) / Z;
-                            qv = exp(dl / (double)row.temperature);
+                            const double dl = (double)key_float(~(uint32_t)(cv >> 32)) - (double)m;
+                            pd[tid] = exp(dl) / Z;
+                            qd[tid] = exp(dl / (double)row.temperature);
                         }
-                        const double runq = block_excl_scan<double>(qv, s, nullptr) + qv;
-                        cut = W;
-                        if (row.top_p < 1.0f) {
-                            const double runp = block_excl_scan<double>(pv, s, nullptr) + pv;
-                            const uint32_t first =
-                                block_min_u((tid < W && runp >= (double)row.top_p) ? tid : 0xFFFFFFFFu, s);
-                            if (first != 0xFFFFFFFFu) cut = first + 1u;
-                        }
-                        if (row.top_k > 0 && cut > (uint32_t)row.top_k) cut = (uint32_t)row.top_k;
-                        if (cut < 1u) cut = 1u;
-                        if (tid == cut - 1u) s.bd[1] = runq;
                         __syncthreads();
-                        denom = s.bd[1];
-                        r = (double)u * denom;
-                        const uint32_t pick = block_min_u((tid < cut && runq >= r) ? tid : 0xFFFFFFFFu, s);
-                        rank = (pick == 0xFFFFFFFFu) ? cut - 1u : pick;
-                        if (tid == rank) s.bu[5] = idi;
+                        if (wave == 0u) {
+                            double rp[kPer], rq[kPer];
+                            double ap = 0.0, aq = 0.0;
+#pragma unroll
+                            for (uint32_t j = 0; j < kPer; ++j) {
+                                const uint32_t i = lane * kPer + j;
+                                ap += (i < W) ? pd[i] : 0.0;
+                                aq += (i < W) ? qd[i] : 0.0;
+                                rp[j] = ap;
+                                rq[j] = aq;
+                            }
+                            const double bp = wave_incl_scan(ap, lane) - ap, bq = wave_incl_scan(aq, lane) - aq;
+#pragma unroll
+                            for (uint32_t j = 0; j < kPer; ++j) {
+                                rp[j] += bp;
+                                rq[j] += bq;
+                            }
+                            uint32_t ct = W;
+                            if (row.top_p < 1.0f) {
+                                uint32_t fj = kPer;  // the lane's first entry whose running p reaches top_p
+#pragma unroll
+                                for (int j = (int)kPer - 1; j >= 0; --j)
+                                    if (lane * kPer + (uint32_t)j < W && rp[j] >= (double)row.top_p) fj = (uint32_t)j;
+                                const unsigned long long mk = __ballot(fj < kPer);
+                                if (mk) {
+                                    const uint32_t L = (uint32_t)__ffsll((long long)mk) - 1u;
+                                    ct = L * kPer + lane_read(fj, (int)L) + 1u;
+                                }
+                            }
+                            if (row.top_k > 0 && ct > (uint32_t)row.top_k) ct = (uint32_t)row.top_k;
+                            if (ct < 1u) ct = 1u;
+                            const uint32_t jc = (ct - 1u) % kPer;
+                            double qc = rq[0];
+#pragma unroll
+                            for (uint32_t j = 1; j < kPer; ++j) qc = (j == jc) ? rq[j] : qc;
+                            const double dn = lane_read(qc, (int)((ct - 1u) / kPer));
+                            const double rr = (double)u * dn;
+                            uint32_t fk = kPer;  // the lane's first entry below the cut reaching r
+#pragma unroll
+                            for (int j = (int)kPer - 1; j >= 0; --j)
+                                if (lane * kPer + (uint32_t)j < ct && rq[j] >= rr) fk = (uint32_t)j;
+                            const unsigned long long mk2 = __ballot(fk < kPer);
+                            uint32_t rk = ct - 1u;
+                            if (mk2) {
+                                const uint32_t L = (uint32_t)__ffsll((long long)mk2) - 1u;
+                                rk = L * kPer + lane_read(fk, (int)L);
+                            }
+                            if (lane == 0u) {
+                                s.bu[5] = (uint32_t)s.cand[rk]; s.bu[6] = ct; s.bu[7] = rk;
+                                s.bd[1] = dn; s.bd[2] = rr;
+                            }
+                        }
                         __syncthreads();
                         token = s.bu[5];
+                        cut = s.bu[6];
+                        rank = s.bu[7];
+                        denom = s.bd[1];
+                        r = s.bd[2];
                     }
                     rep.cut = cut;
                     rep.rank = rank;
