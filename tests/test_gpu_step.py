@@ -646,6 +646,24 @@ def test_full_vocab_one_workgroup_path(head):
     assert np.all(paths == 2), paths
 
 
+@pytest.mark.parametrize("nfv", [12, 40, 64])
+def test_full_vocab_slice_counts(head, nfv):
+    """The number of workgroups per full-vocabulary row follows the number of such rows (256 /
+    n, from 4 to 32): 12 rows take 21 slices, 40 rows 6 and 64 rows 4, slices whose lengths are
+    not powers of two and whose last one is short. Every row gives the oracle sampler's token,
+    and a second call with other uniforms reuses the cleared sums."""
+    h, _ = head
+    base = (synth.normal(11 + nfv, 85, nfv * V).reshape(nfv, V) * 3).astype(np.float32)
+    ts, ps = [1.0, 0.7, 1.3, 0.9], [0.9, 0.95, 0.6, 0.99]
+    for call in range(2):
+        rows = [T.row_default(temperature=ts[b % 4], top_p=ps[(b // 4) % 4], top_k=0, seed=800 + b,
+                              counter=3 + call, flags=T.TURBO_ROW_FULL_VOCAB) for b in range(nfv)]
+        toks, after, rep = sample_given(h, base, rows)
+        assert np.array_equal(after, base)
+        check_sampler_on_gpu_logits(rows, toks, base, [T.row_uniform(r) for r in rows])
+        assert np.all(rep.view(np.uint32)[:, 5] == 2)
+
+
 def test_few_full_vocab_rows_in_a_large_batch(head):
     """A batch above 64 rows with only a few full-vocabulary rows (here 100 rows, of which rows 3,
     50 and 99 sample the whole vocabulary and row 64 is degenerate): those rows still take the
