@@ -853,7 +853,9 @@ TURBO_DT_API int turbo_lmhead_logits(void* handle, const void* x, int x_dtype, i
         throw std::runtime_error("x_dtype must be TURBO_HIDDEN_F32 or TURBO_HIDDEN_BF16");
     tdt::DevRow rows[kMaxBatch];
     for (int b = 0; b < batch; ++b) rows[b] = greedy_devrow(h);
-    launch_greedy_head(*bx, rows, batch, x, x_dtype, epi_args(h, logits, apply_softcap != 0));
+    tdt::EpiArgs ep = epi_args(h, logits, apply_softcap != 0);
+    ep.partials = nullptr;  // no select follows
+    launch_greedy_head(*bx, rows, batch, x, x_dtype, ep);
     return 1;
     API_CATCH(0)
 }

@@ -72,6 +72,7 @@ __device__ inline void finish_wave(float l, uint32_t b, uint32_t tile, uint32_t 
     }
     if (!valid) l = -INFINITY;
     if (ep.logits && valid) ep.logits[(size_t)b * ep.V + id] = l;
+    if (!ep.partials) return;  // a logits-only call: no select reads the block summaries
     const float m = wave_max(l);
     const uint32_t arg = wave_min_u(l == m ? id : 0xFFFFFFFFu);
     const float sm = wave_max(id == arg ? -INFINITY : l);  // a repeat of the maximum counts

@@ -100,7 +100,7 @@ struct EpiArgs {
     uint32_t ntile;
     float cap;                 // softcap applied to the raw accumulator (0 = skip)
     float* logits;             // [B][V] or null (not written)
-    BlockPartial* partials;    // [B][ntile]
+    BlockPartial* partials;    // [B][ntile], or null for a logits-only call (not written)
     const DevRow* rows;        // [B]
     const ModEntry* mods;      // [B][mod_cap] bias tables (rows with has_mods & 2)
     uint32_t mod_cap;

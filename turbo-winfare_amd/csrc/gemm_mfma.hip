@@ -447,61 +447,63 @@ __global__ __launch_bounds__(64 * WV, OCC) void k_head_mfma(
             for (int i = 0; i < 32; ++i)
                 if (base + 32u * (i >> 4) + acc_row(i & 15, hl) >= ep.V) zz[i] = -INFINITY;
         }
-        // Block statistics over the 64 rows: the lane's 32 values, then the other half of the
-        // column (lane ^ 32).
-        float lmax, lsec = -INFINITY;
-        if (!ep.no_smax) {
-            // running maximum and second maximum (repeats count), two values at a time
-            lmax = -INFINITY;
+        // Block statistics over the 64 rows (not for a logits-only call, which no select reads):
+        // the lane's 32 values, then the other half of the column (lane ^ 32).
+        if (ep.partials) {
+            float lmax, lsec = -INFINITY;
+            if (!ep.no_smax) {
+                // running maximum and second maximum (repeats count), two values at a time
+                lmax = -INFINITY;
 #pragma unroll
-            for (int i = 0; i < 32; i += 2) {
-                const float hi = fmaxf(zz[i], zz[i + 1]), lo = fminf(zz[i], zz[i + 1]);
-                lsec = fmaxf(fmaxf(lsec, lo), fminf(lmax, hi));
-                lmax = fmaxf(lmax, hi);
+                for (int i = 0; i < 32; i += 2) {
+                    const float hi = fmaxf(zz[i], zz[i + 1]), lo = fminf(zz[i], zz[i + 1]);
+                    lsec = fmaxf(fmaxf(lsec, lo), fminf(lmax, hi));
+                    lmax = fmaxf(lmax, hi);
+                }
+            } else {
+                lmax = zz[0];
+#pragma unroll
+                for (int i = 1; i < 32; ++i) lmax = fmaxf(lmax, zz[i]);
             }
-        } else {
-            lmax = zz[0];
+            const float om = xor32(lmax);
+            const float bm = fmaxf(lmax, om);  // the block maximum
+            // lowest row of the lane holding it, then the lower of the two halves' ids
+            uint32_t ri = 32u;
 #pragma unroll
-            for (int i = 1; i < 32; ++i) lmax = fmaxf(lmax, zz[i]);
-        }
-        const float om = xor32(lmax);
-        const float bm = fmaxf(lmax, om);  // the block maximum
-        // lowest row of the lane holding it, then the lower of the two halves' ids
-        uint32_t ri = 32u;
+            for (int i = 31; i >= 0; --i) ri = (zz[i] == bm) ? (uint32_t)i : ri;
+            uint32_t barg = (ri < 32u) ? base + 32u * (ri >> 4) + acc_row((int)(ri & 15u), hl) : 0xFFFFFFFFu;
+            barg = min(barg, xor32(barg));
+            float bsec = -INFINITY;
+            if (!ep.no_smax) bsec = fmaxf(fmaxf(lsec, xor32(lsec)), fminf(lmax, om));
+            float bmin;
+            if (may_ninf) {
+                bmin = INFINITY;
 #pragma unroll
-        for (int i = 31; i >= 0; --i) ri = (zz[i] == bm) ? (uint32_t)i : ri;
-        uint32_t barg = (ri < 32u) ? base + 32u * (ri >> 4) + acc_row((int)(ri & 15u), hl) : 0xFFFFFFFFu;
-        barg = min(barg, xor32(barg));
-        float bsec = -INFINITY;
-        if (!ep.no_smax) bsec = fmaxf(fmaxf(lsec, xor32(lsec)), fminf(lmax, om));
-        float bmin;
-        if (may_ninf) {
-            bmin = INFINITY;
+                for (int i = 0; i < 32; ++i) bmin = fminf(bmin, zz[i] == -INFINITY ? INFINITY : zz[i]);
+            } else {
+                bmin = zz[0];
 #pragma unroll
-            for (int i = 0; i < 32; ++i) bmin = fminf(bmin, zz[i] == -INFINITY ? INFINITY : zz[i]);
-        } else {
-            bmin = zz[0];
-#pragma unroll
-            for (int i = 1; i < 32; ++i) bmin = fminf(bmin, zz[i]);
-        }
-        bmin = fminf(bmin, xor32(bmin));
-        float se = 0.0f;
-        if (!ep.no_sumexp) {
-            if (bm != -INFINITY) {
-                const float mb2 = bm * 1.4426950408889634f;
-#pragma unroll
-                for (int i = 0; i < 32; ++i) se += __builtin_amdgcn_exp2f(fmaf(zz[i], 1.4426950408889634f, -mb2));
+                for (int i = 1; i < 32; ++i) bmin = fminf(bmin, zz[i]);
             }
-            se += xor32(se);
-        }
-        if (col_ok && hl == 0u) {
-            BlockPartial bp;
-            bp.max = bm;
-            bp.arg = (bm == -INFINITY) ? base : barg;
-            bp.sumexp = se;
-            bp.minf = bmin;
-            bp.smax = bsec;
-            ep.partials[(size_t)bq * ep.ntile + tile] = bp;
+            bmin = fminf(bmin, xor32(bmin));
+            float se = 0.0f;
+            if (!ep.no_sumexp) {
+                if (bm != -INFINITY) {
+                    const float mb2 = bm * 1.4426950408889634f;
+#pragma unroll
+                    for (int i = 0; i < 32; ++i) se += __builtin_amdgcn_exp2f(fmaf(zz[i], 1.4426950408889634f, -mb2));
+                }
+                se += xor32(se);
+            }
+            if (col_ok && hl == 0u) {
+                BlockPartial bp;
+                bp.max = bm;
+                bp.arg = (bm == -INFINITY) ? base : barg;
+                bp.sumexp = se;
+                bp.minf = bmin;
+                bp.smax = bsec;
+                ep.partials[(size_t)bq * ep.ntile + tile] = bp;
+            }
         }
         // Logits: each 32-row half goes through the wave's own LDS tile (32 columns x 32 rows,
         // 16-byte pieces XOR-swizzled so that neither side conflicts), so one float4 store
